@@ -1,0 +1,171 @@
+/*
+ * seedvr2_awa.h — C ABI of the MI355X (gfx950) adaptive-window-attention path.
+ *
+ * This is the boundary a host (C, C++, ctypes, ...) binds to replace the
+ * reference's AWA operator chain
+ *   SeedVR2AWAPack -> SeedVR2MMRoPE -> SeedVR2WindowAttention -> SeedVR2AWAUnpack
+ * (src/awa/awa_layers.h:47-220, src/awa/awa_layers.cpp:363-1291) and the
+ * Vulkan memory/sync helpers it relies on (src/vulkan/transient_staging_allocator.h:10-23,
+ * src/inference/vulkan_benchmark.h:22-31). Every entry point uses plain
+ * pointers, sizes and the descriptor structs below; no C++ or framework types.
+ *
+ * Conventions
+ *  - Return codes follow the reference layers: 0 success, -1 invalid argument,
+ *    shape or state (src/awa/awa_layers.cpp:423-434, :506-525), -100 allocation
+ *    failure (:438-439). AWA_ERR_DEVICE (-2) reports a HIP runtime error, which
+ *    has no reference counterpart. awa_last_error() returns the diagnostic of
+ *    the calling thread's last failure.
+ *  - Device work is enqueued on the given stream (NULL = the default stream)
+ *    and is asynchronous; the caller synchronises (awa_stream_synchronize
+ *    replaces the reference's submit_and_wait_profiled).
+ *  - Plans are immutable after awa_plan_upload except for their device
+ *    workspace: calls that use one plan on several streams at once race on it.
+ */
+#ifndef SEEDVR2_AWA_H
+#define SEEDVR2_AWA_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AWA_OK 0
+#define AWA_ERR_INVALID (-1)
+#define AWA_ERR_DEVICE (-2)
+#define AWA_ERR_ALLOC (-100)
+
+/* Arithmetic of the attention contractions. AWA_COMPUTE_F32 runs QK^T and PV
+ * on fp32 MFMA (the reference's FP32 blocks); AWA_COMPUTE_BF16 rounds Q, K, V
+ * and P to bf16 and accumulates in fp32 on bf16 MFMA (BF16 blocks). Softmax
+ * statistics are fp32 in both. */
+#define AWA_COMPUTE_F32 0
+#define AWA_COMPUTE_BF16 1
+
+/* A device blob described the way an ncnn Mat is (elempack 1):
+ * dims 1..4 with extents w (fastest), h, d, c; n batches (NCNN_BATCH, 1 when
+ * unused); cstep / nstep in elements; elemsize 4 (fp32) or 2 (bf16). */
+typedef struct awa_blob {
+    void* data;
+    int dims;
+    int w, h, d, c;
+    int n;
+    int elemsize;
+    long long cstep;
+    long long nstep;
+} awa_blob;
+
+/* Layer parameters, with the reference's param ids (src/awa/awa_layers.cpp:90-114, :872):
+ * 0/1/2 source_t/h/w (-1,-1,-1 = take them from the runtime spec, as the
+ * dynamic model package does), 3/4/5 window COUNTS along t/h/w over the grid
+ * rescaled to area 45x80, 6 text tokens, 7 shifted, 8 rope_dim (0 = default 126).
+ * runtime_* is the AwaRuntimeSpec (src/awa/awa_layers.h:31-39); set
+ * runtime_tokens = 0 when there is none. */
+typedef struct awa_plan_desc {
+    int source_t, source_h, source_w;
+    int windows_t, windows_h, windows_w;
+    int text_tokens;
+    int shifted;
+    int rope_dim;
+    int runtime_t, runtime_h, runtime_w, runtime_tokens;
+} awa_plan_desc;
+
+typedef struct awa_plan_info {
+    int source_t, source_h, source_w;
+    int source_tokens;     /* N = t*h*w */
+    int text_tokens;       /* T_x */
+    int window_count;      /* nwin */
+    int sequence_tokens;   /* S = N + nwin*T_x (packed rows) */
+    int window_t, window_h, window_w; /* unclipped window extents */
+    int max_window_tokens; /* max L over windows */
+    int rope_dim;
+    int shifted;
+} awa_plan_info;
+
+typedef struct awa_plan awa_plan;
+
+/* ---- runtime: device, memory, streams, events (replaces src/vulkan for this path) ---- */
+
+const char* awa_last_error(void);
+int awa_device_count(int* count);
+/* Selects the device for the calling thread and caches its properties. */
+int awa_runtime_init(int device);
+int awa_malloc(void** ptr, size_t bytes);
+int awa_free(void* ptr);
+/* Pinned host memory for staging (allocated, never registered). */
+int awa_host_alloc(void** ptr, size_t bytes);
+int awa_host_free(void* ptr);
+int awa_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
+int awa_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
+int awa_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+/* Fills bytes with zero using a kernel (safe inside captured graphs). */
+int awa_zero(void* dst, size_t bytes, void* stream);
+int awa_stream_create(void** stream);
+int awa_stream_destroy(void* stream);
+int awa_stream_synchronize(void* stream);
+int awa_event_create(void** event);
+int awa_event_destroy(void* event);
+int awa_event_record(void* event, void* stream);
+int awa_event_synchronize(void* event);
+int awa_event_elapsed_ms(void* start, void* stop, float* ms);
+/* Seeded N(0,1) synthetic data on the device (counter-based, Box-Muller);
+ * elemsize 4 or 2 (bf16, rounded to nearest even). Used to build benchmark
+ * inputs; parity tests use the host generator of the reference instead. */
+int awa_fill_normal(void* dst, size_t count, int elemsize, unsigned long long seed, void* stream);
+
+/* ---- plan: windows, index maps, RoPE tables (the layers' load_param/upload_model) ---- */
+
+/* Builds the window partition and every map on the host
+ * (src/awa/awa_layers.cpp:53-88, :382-417, :599-636, :867-911, :1046-1060). */
+int awa_plan_create(const awa_plan_desc* desc, awa_plan** plan);
+void awa_plan_destroy(awa_plan* plan);
+int awa_plan_info_get(const awa_plan* plan, awa_plan_info* info);
+/* Host copies of the plan's tables, all int32 unless stated:
+ * windows: 6 ints (t0,t1,h0,h1,w0,w1) per window, w-outer/h/t-inner order;
+ * sequence_index[S]: source row of each packed row (video index, or N + text k);
+ * cu_seqlens[nwin+1]; video_positions[N]: packed row of each video token;
+ * text_positions[nwin*T_x]; rope_table: float [S][2*rope_dim] = cos | sin rows
+ * exactly as the reference's rotation Mat. */
+int awa_plan_windows(const awa_plan* plan, int* out);
+int awa_plan_sequence_index(const awa_plan* plan, int* out);
+int awa_plan_cu_seqlens(const awa_plan* plan, int* out);
+int awa_plan_video_positions(const awa_plan* plan, int* out);
+int awa_plan_text_positions(const awa_plan* plan, int* out);
+int awa_plan_rope_table(const awa_plan* plan, float* out);
+/* Copies the plan's device tables to the current device (upload_model). */
+int awa_plan_upload(awa_plan* plan, void* stream);
+
+/* ---- forward entry points ---- */
+
+/* Fused layer: gather + MMRoPE + window attention + scatter + text mean in one
+ * pass, equivalent to Pack -> MMRoPE -> WindowAttention -> Unpack.
+ * video_qkv: the four QKV layouts of describe_qkv_layout (src/awa/awa_layers.cpp:116-170)
+ *   over N tokens; text_qkv: the same over T_x tokens; fp32 or bf16.
+ * video_out: Mat(d, H, N) (dims 3) or the NCNN_BATCH Mat(d, H, w, h; n = t)
+ *   (dims 4); text_out: Mat(d, H, T_x); fp32 or bf16 (bf16 rounds to nearest even).
+ * Requires head_dim 128 and rope_dim 126; other shapes use the staged entry points. */
+int awa_forward(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv, const awa_blob* video_out,
+                const awa_blob* text_out, int compute, void* stream);
+
+/* SeedVR2AWAPack (src/awa/awa_layers.cpp:419-458, :501-578): packed = Mat(d, 3H, S)
+ * fp32, cu_seqlens = Mat(nwin+1) fp32. */
+int awa_pack(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv, const awa_blob* packed,
+             const awa_blob* cu_seqlens, void* stream);
+/* SeedVR2MMRoPE (:913-953, :985-1025): Mat(d, 3H, S) fp32/bf16 -> fp32. */
+int awa_mmrope(const awa_plan* plan, const awa_blob* input, const awa_blob* output, void* stream);
+/* SeedVR2WindowAttention (:1062-1120, :1152-1234): Mat(d, 3H, S) -> Mat(d, H, S). */
+int awa_window_attention(const awa_plan* plan, const awa_blob* input, const awa_blob* output, int compute,
+                         void* stream);
+/* SeedVR2AWAUnpack (:638-689, :743-846): Mat(d, H, S) -> video, text as in awa_forward;
+ * text = (sum over windows in window order) / nwin. */
+int awa_unpack(const awa_plan* plan, const awa_blob* packed, const awa_blob* video_out, const awa_blob* text_out,
+               void* stream);
+/* Element cast fp32 <-> bf16 honouring cstep/nstep (record_awa_cast, :301-332;
+ * the block-9 precision switch convert_precision_gpu, src/dit/dit_stack.cpp:329-357). */
+int awa_cast(const awa_blob* input, const awa_blob* output, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SEEDVR2_AWA_H */

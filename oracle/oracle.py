@@ -1,0 +1,229 @@
+"""ctypes/numpy view of the CPU oracle (test infrastructure only).
+
+Only tests, the smoke check and the CPU-baseline leg of ``bench.py`` use this
+module, always as the checker. It wraps ``liboracle_awa.so`` built from
+``awa_oracle.cpp`` (``make -C oracle``); every function there cites the
+reference code it restates.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+_REF = None
+
+_i = ctypes.c_int
+_ll = ctypes.c_longlong
+_p = ctypes.c_void_p
+
+
+def lib() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is None:
+        path = os.path.join(HERE, "liboracle_awa.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"oracle library missing: {path} (run `make -C oracle`)")
+        _LIB = ctypes.CDLL(path)
+        _LIB.orc_python_round_positive.argtypes = [ctypes.c_double]
+        _LIB.orc_make_windows.argtypes = [_i] * 7 + [_p, _i]
+        _LIB.orc_map_sizes.argtypes = [_i] * 8 + [_p]
+        _LIB.orc_build_maps.argtypes = [_i] * 8 + [_p] * 5
+        _LIB.orc_rope_table.argtypes = [_i] * 9 + [_p]
+        _LIB.orc_pack_forward.argtypes = [_p, _ll, _ll, _p, _ll, _ll, _p, _i, _p, _i, _i, _i, _i, _p, _p]
+        _LIB.orc_mmrope_forward.argtypes = [_p, _p, _i, _i, _i, _i, _p]
+        _LIB.orc_attention_cpu.argtypes = [_p, _p, _i, _i, _i, _p]
+        _LIB.orc_attention_kahan.argtypes = [_p, _p, _i, _i, _i, _p]
+        _LIB.orc_unpack_forward.argtypes = [_p, _p, _i, _p, _i, _i, _i, _i, _i, _p, _p]
+        _LIB.orc_fill_gaussian.argtypes = [_p, _ll, ctypes.c_uint, ctypes.c_ulonglong]
+        _LIB.orc_seed_seq_words.argtypes = [ctypes.c_uint, ctypes.c_ulonglong, _p]
+        _LIB.orc_round_bf16.argtypes = [_p, _p, _ll]
+        _LIB.orc_awa_layer.argtypes = [_p, _p] + [_i] * 13 + [_p, _p]
+    return _LIB
+
+
+def ref_sampler():
+    """The reference's own fill_gaussian_noise built in oracle/_ref, or None."""
+    global _REF
+    if _REF is None:
+        path = os.path.join(HERE, "_ref", "libref_sampler.so")
+        if not os.path.exists(path):
+            return None
+        _REF = ctypes.CDLL(path)
+        _REF.ref_fill_gaussian_noise.argtypes = [_p, ctypes.c_ulonglong, ctypes.c_uint, ctypes.c_ulonglong]
+    return _REF
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+@dataclass(frozen=True)
+class Geometry:
+    """One AWA layer's parameters (the reference's layer params 0-7)."""
+
+    t: int
+    h: int
+    w: int
+    nt: int
+    nh: int
+    nw: int
+    text_tokens: int
+    shifted: bool
+
+    @property
+    def args(self):
+        return (self.t, self.h, self.w, self.nt, self.nh, self.nw)
+
+    @property
+    def source_tokens(self) -> int:
+        return self.t * self.h * self.w
+
+
+def python_round_positive(x: float) -> int:
+    return lib().orc_python_round_positive(float(x))
+
+
+def make_windows(g: Geometry) -> np.ndarray:
+    cap = 1 << 16
+    out = np.zeros((cap, 6), dtype=np.int32)
+    n = lib().orc_make_windows(*g.args, int(g.shifted), _ptr(out), cap)
+    if n < 0:
+        raise ValueError("invalid window arguments")
+    return out[:n].copy()
+
+
+@dataclass
+class Maps:
+    sequence_index: np.ndarray
+    cu_seqlens: np.ndarray
+    video_positions: np.ndarray
+    text_positions: np.ndarray
+    target: np.ndarray
+    status: int
+
+    @property
+    def window_count(self) -> int:
+        return len(self.cu_seqlens) - 1
+
+    @property
+    def sequence_tokens(self) -> int:
+        return len(self.sequence_index)
+
+
+def build_maps(g: Geometry) -> Maps:
+    sizes = np.zeros(2, dtype=np.int32)
+    lib().orc_map_sizes(*g.args, g.text_tokens, int(g.shifted), _ptr(sizes))
+    S, nwin = int(sizes[0]), int(sizes[1])
+    N = g.source_tokens
+    seq = np.zeros(S, np.int32)
+    cu = np.zeros(nwin + 1, np.int32)
+    vpos = np.zeros(N, np.int32)
+    tpos = np.zeros(nwin * g.text_tokens, np.int32)
+    target = np.zeros(N, np.int32)
+    st = lib().orc_build_maps(*g.args, g.text_tokens, int(g.shifted), _ptr(seq), _ptr(cu), _ptr(vpos),
+                              _ptr(tpos), _ptr(target))
+    return Maps(seq, cu, vpos, tpos, target, st)
+
+
+def rope_table(g: Geometry, rope_dim: int = 126) -> np.ndarray:
+    m = build_maps(g)
+    out = np.zeros((m.sequence_tokens, 2 * rope_dim), np.float32)
+    n = lib().orc_rope_table(*g.args, g.text_tokens, int(g.shifted), rope_dim, _ptr(out))
+    if n != m.sequence_tokens:
+        raise ValueError("invalid rope_dim")
+    return out
+
+
+def pack_forward(g: Geometry, video: np.ndarray, text: np.ndarray, heads: int, head_dim: int):
+    """video [N][3][H][d], text [T_x][3][H][d] fp32 -> packed [S][3][H][d], cu float."""
+    m = build_maps(g)
+    video = np.ascontiguousarray(video, np.float32)
+    text = np.ascontiguousarray(text, np.float32)
+    row = 3 * heads * head_dim
+    packed = np.zeros((m.sequence_tokens, 3, heads, head_dim), np.float32)
+    cu = np.zeros(m.window_count + 1, np.float32)
+    lib().orc_pack_forward(_ptr(video), row, heads * head_dim, _ptr(text), row, heads * head_dim,
+                           _ptr(m.sequence_index), m.sequence_tokens, _ptr(m.cu_seqlens), m.window_count,
+                           g.source_tokens, heads, head_dim, _ptr(packed), _ptr(cu))
+    return packed, cu
+
+
+def mmrope_forward(packed: np.ndarray, table: np.ndarray, heads: int, head_dim: int, rope_dim: int = 126):
+    packed = np.ascontiguousarray(packed, np.float32)
+    out = np.zeros_like(packed)
+    lib().orc_mmrope_forward(_ptr(packed), _ptr(np.ascontiguousarray(table, np.float32)), packed.shape[0], heads,
+                             head_dim, rope_dim, _ptr(out))
+    return out
+
+
+def attention(packed: np.ndarray, cu_seqlens: np.ndarray, heads: int, head_dim: int, order: str = "kahan"):
+    """packed [S][3][H][d] -> [S][H][d]; order 'cpu' (loop order) or 'kahan' (shader order)."""
+    packed = np.ascontiguousarray(packed, np.float32)
+    cu = np.ascontiguousarray(cu_seqlens, np.int32)
+    out = np.zeros((packed.shape[0], heads, head_dim), np.float32)
+    fn = lib().orc_attention_cpu if order == "cpu" else lib().orc_attention_kahan
+    fn(_ptr(packed), _ptr(cu), len(cu) - 1, heads, head_dim, _ptr(out))
+    return out
+
+
+def unpack_forward(g: Geometry, packed_out: np.ndarray, heads: int, head_dim: int, text_order: str = "gpu"):
+    """packed [S][H][d] -> video [N][H][d], text [T_x][H][d]; text_order 'cpu' or 'gpu'."""
+    m = build_maps(g)
+    packed_out = np.ascontiguousarray(packed_out, np.float32)
+    video = np.zeros((g.source_tokens, heads, head_dim), np.float32)
+    text = np.zeros((g.text_tokens, heads, head_dim), np.float32)
+    lib().orc_unpack_forward(_ptr(packed_out), _ptr(m.video_positions), g.source_tokens, _ptr(m.text_positions),
+                             g.text_tokens, m.window_count, heads, head_dim, 0 if text_order == "cpu" else 1,
+                             _ptr(video), _ptr(text))
+    return video, text
+
+
+def awa_layer(g: Geometry, video_qkv: np.ndarray, text_qkv: np.ndarray, heads: int, head_dim: int,
+              rope_dim: int = 126, attention_order: str = "kahan", text_order: str = "gpu"):
+    """Whole chain Pack -> MMRoPE -> WindowAttention -> Unpack on fp32 inputs."""
+    video_qkv = np.ascontiguousarray(video_qkv, np.float32)
+    text_qkv = np.ascontiguousarray(text_qkv, np.float32)
+    video = np.zeros((g.source_tokens, heads, head_dim), np.float32)
+    text = np.zeros((g.text_tokens, heads, head_dim), np.float32)
+    rc = lib().orc_awa_layer(_ptr(video_qkv), _ptr(text_qkv), *g.args, g.text_tokens, int(g.shifted), rope_dim,
+                             heads, head_dim, 0 if attention_order == "cpu" else 1,
+                             0 if text_order == "cpu" else 1, _ptr(video), _ptr(text))
+    if rc != 0:
+        raise ValueError("oracle layer failed")
+    return video, text
+
+
+def fill_gaussian(count: int, seed: int, stream: int = 0) -> np.ndarray:
+    out = np.zeros(count, np.float32)
+    if lib().orc_fill_gaussian(_ptr(out), count, seed, stream) != 0:
+        raise ValueError("invalid noise request")
+    return out
+
+
+def seed_seq_words(seed: int, stream: int) -> np.ndarray:
+    out = np.zeros(624, np.uint32)
+    lib().orc_seed_seq_words(seed, stream, _ptr(out))
+    return out
+
+
+def round_bf16_bits(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(x.shape, np.uint16)
+    lib().orc_round_bf16(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (bits.astype(np.uint32) << 16).view(np.float32)
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    """fp32 values rounded to the nearest bf16 (ties to even), returned as fp32."""
+    return bf16_bits_to_f32(round_bf16_bits(x))

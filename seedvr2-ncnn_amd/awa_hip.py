@@ -1,0 +1,357 @@
+"""Python (ctypes) binding of libseedvr2_awa.so, the C ABI declared in
+include/seedvr2_awa.h.
+
+This is the Python-side mirror a ctypes caller (for example the reference's
+Python tooling) would use. It exposes plans, device buffers, streams/events
+and the forward entry points; it never computes anything itself. The library
+is loaded from this directory and the import fails loudly when it is missing.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libseedvr2_awa.so")
+
+AWA_OK = 0
+AWA_ERR_INVALID = -1
+AWA_ERR_DEVICE = -2
+AWA_ERR_ALLOC = -100
+COMPUTE_F32 = 0
+COMPUTE_BF16 = 1
+
+# Every symbol of include/seedvr2_awa.h.
+EXPORTED_SYMBOLS = (
+    "awa_last_error", "awa_device_count", "awa_runtime_init", "awa_malloc", "awa_free", "awa_host_alloc",
+    "awa_host_free", "awa_memcpy_h2d", "awa_memcpy_d2h", "awa_memcpy_d2d", "awa_zero", "awa_stream_create",
+    "awa_stream_destroy", "awa_stream_synchronize", "awa_event_create", "awa_event_destroy", "awa_event_record",
+    "awa_event_synchronize", "awa_event_elapsed_ms", "awa_fill_normal", "awa_plan_create", "awa_plan_destroy",
+    "awa_plan_info_get", "awa_plan_windows", "awa_plan_sequence_index", "awa_plan_cu_seqlens",
+    "awa_plan_video_positions", "awa_plan_text_positions", "awa_plan_rope_table", "awa_plan_upload",
+    "awa_forward", "awa_pack", "awa_mmrope", "awa_window_attention", "awa_unpack", "awa_cast",
+)
+
+
+class AwaBlob(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("dims", ctypes.c_int),
+        ("w", ctypes.c_int),
+        ("h", ctypes.c_int),
+        ("d", ctypes.c_int),
+        ("c", ctypes.c_int),
+        ("n", ctypes.c_int),
+        ("elemsize", ctypes.c_int),
+        ("cstep", ctypes.c_longlong),
+        ("nstep", ctypes.c_longlong),
+    ]
+
+
+class AwaPlanDesc(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_int) for name in (
+        "source_t", "source_h", "source_w", "windows_t", "windows_h", "windows_w", "text_tokens", "shifted",
+        "rope_dim", "runtime_t", "runtime_h", "runtime_w", "runtime_tokens")]
+
+
+class AwaPlanInfo(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_int) for name in (
+        "source_t", "source_h", "source_w", "source_tokens", "text_tokens", "window_count", "sequence_tokens",
+        "window_t", "window_h", "window_w", "max_window_tokens", "rope_dim", "shifted")]
+
+
+_LIB: Optional[ctypes.CDLL] = None
+
+
+def lib() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -C seedvr2-ncnn_amd`")
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+        L.awa_last_error.restype = ctypes.c_char_p
+        L.awa_device_count.argtypes = [ctypes.POINTER(i)]
+        L.awa_runtime_init.argtypes = [i]
+        L.awa_malloc.argtypes = [ctypes.POINTER(vp), sz]
+        L.awa_free.argtypes = [vp]
+        L.awa_host_alloc.argtypes = [ctypes.POINTER(vp), sz]
+        L.awa_host_free.argtypes = [vp]
+        for name in ("awa_memcpy_h2d", "awa_memcpy_d2h", "awa_memcpy_d2d"):
+            getattr(L, name).argtypes = [vp, vp, sz, vp]
+        L.awa_zero.argtypes = [vp, sz, vp]
+        L.awa_stream_create.argtypes = [ctypes.POINTER(vp)]
+        L.awa_stream_destroy.argtypes = [vp]
+        L.awa_stream_synchronize.argtypes = [vp]
+        L.awa_event_create.argtypes = [ctypes.POINTER(vp)]
+        L.awa_event_destroy.argtypes = [vp]
+        L.awa_event_record.argtypes = [vp, vp]
+        L.awa_event_synchronize.argtypes = [vp]
+        L.awa_event_elapsed_ms.argtypes = [vp, vp, ctypes.POINTER(ctypes.c_float)]
+        L.awa_fill_normal.argtypes = [vp, sz, i, ctypes.c_ulonglong, vp]
+        L.awa_plan_create.argtypes = [ctypes.POINTER(AwaPlanDesc), ctypes.POINTER(vp)]
+        L.awa_plan_destroy.argtypes = [vp]
+        L.awa_plan_destroy.restype = None
+        L.awa_plan_info_get.argtypes = [vp, ctypes.POINTER(AwaPlanInfo)]
+        for name in ("awa_plan_windows", "awa_plan_sequence_index", "awa_plan_cu_seqlens",
+                     "awa_plan_video_positions", "awa_plan_text_positions"):
+            getattr(L, name).argtypes = [vp, vp]
+        L.awa_plan_rope_table.argtypes = [vp, vp]
+        L.awa_plan_upload.argtypes = [vp, vp]
+        bp = ctypes.POINTER(AwaBlob)
+        L.awa_forward.argtypes = [vp, bp, bp, bp, bp, i, vp]
+        L.awa_pack.argtypes = [vp, bp, bp, bp, bp, vp]
+        L.awa_mmrope.argtypes = [vp, bp, bp, vp]
+        L.awa_window_attention.argtypes = [vp, bp, bp, i, vp]
+        L.awa_unpack.argtypes = [vp, bp, bp, bp, vp]
+        L.awa_cast.argtypes = [bp, bp, vp]
+        _LIB = L
+    return _LIB
+
+
+class AwaError(RuntimeError):
+    def __init__(self, code: int, where: str):
+        msg = lib().awa_last_error().decode(errors="replace")
+        super().__init__(f"{where} failed with {code}: {msg}")
+        self.code = code
+
+
+def check(code: int, where: str) -> None:
+    if code != AWA_OK:
+        raise AwaError(code, where)
+
+
+def device_count() -> int:
+    n = ctypes.c_int(0)
+    check(lib().awa_device_count(ctypes.byref(n)), "awa_device_count")
+    return n.value
+
+
+def init(device: int = 0) -> None:
+    check(lib().awa_runtime_init(device), "awa_runtime_init")
+
+
+# ---- device memory ----
+
+class DeviceBuffer:
+    """Owned device allocation."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = ctypes.c_void_p()
+        check(lib().awa_malloc(ctypes.byref(p), self.nbytes), "awa_malloc")
+        self.ptr = p.value or 0
+
+    def free(self) -> None:
+        if self.ptr:
+            lib().awa_free(ctypes.c_void_p(self.ptr))
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def upload(self, array: np.ndarray, stream: Optional["Stream"] = None) -> None:
+        a = np.ascontiguousarray(array)
+        assert a.nbytes <= self.nbytes
+        check(lib().awa_memcpy_h2d(ctypes.c_void_p(self.ptr), a.ctypes.data_as(ctypes.c_void_p), a.nbytes,
+                                   _s(stream)), "awa_memcpy_h2d")
+        synchronize(stream)
+
+    def download(self, shape, dtype, stream: Optional["Stream"] = None) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        assert out.nbytes <= self.nbytes
+        check(lib().awa_memcpy_d2h(out.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(self.ptr), out.nbytes,
+                                   _s(stream)), "awa_memcpy_d2h")
+        synchronize(stream)
+        return out
+
+    def zero(self, stream: Optional["Stream"] = None) -> None:
+        check(lib().awa_zero(ctypes.c_void_p(self.ptr), self.nbytes, _s(stream)), "awa_zero")
+
+    def fill_normal(self, count: int, elemsize: int, seed: int, stream: Optional["Stream"] = None) -> None:
+        check(lib().awa_fill_normal(ctypes.c_void_p(self.ptr), count, elemsize, seed, _s(stream)),
+              "awa_fill_normal")
+
+
+class Stream:
+    def __init__(self):
+        p = ctypes.c_void_p()
+        check(lib().awa_stream_create(ctypes.byref(p)), "awa_stream_create")
+        self.handle = p.value
+
+    def synchronize(self) -> None:
+        check(lib().awa_stream_synchronize(ctypes.c_void_p(self.handle)), "awa_stream_synchronize")
+
+    def destroy(self) -> None:
+        if self.handle:
+            lib().awa_stream_destroy(ctypes.c_void_p(self.handle))
+            self.handle = None
+
+
+class Event:
+    def __init__(self):
+        p = ctypes.c_void_p()
+        check(lib().awa_event_create(ctypes.byref(p)), "awa_event_create")
+        self.handle = p.value
+
+    def record(self, stream: Optional[Stream] = None) -> None:
+        check(lib().awa_event_record(ctypes.c_void_p(self.handle), _s(stream)), "awa_event_record")
+
+    def synchronize(self) -> None:
+        check(lib().awa_event_synchronize(ctypes.c_void_p(self.handle)), "awa_event_synchronize")
+
+    def elapsed_ms(self, stop: "Event") -> float:
+        ms = ctypes.c_float()
+        check(lib().awa_event_elapsed_ms(ctypes.c_void_p(self.handle), ctypes.c_void_p(stop.handle),
+                                         ctypes.byref(ms)), "awa_event_elapsed_ms")
+        return float(ms.value)
+
+    def destroy(self) -> None:
+        if self.handle:
+            lib().awa_event_destroy(ctypes.c_void_p(self.handle))
+            self.handle = None
+
+
+def _s(stream: Optional[Stream]) -> ctypes.c_void_p:
+    return ctypes.c_void_p(stream.handle if stream is not None else None)
+
+
+def synchronize(stream: Optional[Stream] = None) -> None:
+    check(lib().awa_stream_synchronize(_s(stream)), "awa_stream_synchronize")
+
+
+# ---- blob descriptors (ncnn Mat semantics) ----
+
+def align_cstep(elems: int, elemsize: int) -> int:
+    """ncnn's cstep: channel size rounded up to 16 bytes, in elements."""
+    return ((elems * elemsize + 15) // 16 * 16) // elemsize
+
+
+def mat(ptr: int, w: int, h: int = 1, c: int = 1, elemsize: int = 4, d: int = 1, dims: Optional[int] = None,
+        n: int = 1, cstep: Optional[int] = None, nstep: Optional[int] = None) -> AwaBlob:
+    if dims is None:
+        dims = 4 if d > 1 else (3 if c > 1 else (2 if h > 1 else 1))
+    plane = w * (h if dims >= 2 else 1) * (d if dims == 4 else 1)
+    cs = cstep if cstep is not None else (align_cstep(plane, elemsize) if dims >= 3 else plane)
+    ns = nstep if nstep is not None else cs * (c if dims >= 3 else 1)
+    return AwaBlob(ptr, dims, w, h, d, c, n, elemsize, cs, ns)
+
+
+# ---- plans ----
+
+@dataclass(frozen=True)
+class LayerParams:
+    """The reference layer's params 0-8 (src/awa/awa_layers.cpp:90-114, :872)."""
+
+    t: int
+    h: int
+    w: int
+    nt: int
+    nh: int
+    nw: int
+    text_tokens: int
+    shifted: bool = False
+    rope_dim: int = 126
+
+
+class Plan:
+    def __init__(self, params: LayerParams, runtime: Optional[Sequence[int]] = None):
+        desc = AwaPlanDesc(params.t, params.h, params.w, params.nt, params.nh, params.nw, params.text_tokens,
+                           int(params.shifted), params.rope_dim, 0, 0, 0, 0)
+        if runtime is not None:
+            desc.runtime_t, desc.runtime_h, desc.runtime_w, desc.runtime_tokens = runtime
+        p = ctypes.c_void_p()
+        check(lib().awa_plan_create(ctypes.byref(desc), ctypes.byref(p)), "awa_plan_create")
+        self.handle = p.value
+        info = AwaPlanInfo()
+        check(lib().awa_plan_info_get(ctypes.c_void_p(self.handle), ctypes.byref(info)), "awa_plan_info_get")
+        self.info = info
+
+    def destroy(self) -> None:
+        if self.handle:
+            lib().awa_plan_destroy(ctypes.c_void_p(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+    @property
+    def h(self) -> ctypes.c_void_p:
+        return ctypes.c_void_p(self.handle)
+
+    def _table(self, fn, count, dtype=np.int32, shape=None):
+        out = np.zeros(count if shape is None else shape, dtype)
+        check(fn(self.h, out.ctypes.data_as(ctypes.c_void_p)), fn.__name__)
+        return out
+
+    def windows(self) -> np.ndarray:
+        return self._table(lib().awa_plan_windows, None, shape=(self.info.window_count, 6))
+
+    def sequence_index(self) -> np.ndarray:
+        return self._table(lib().awa_plan_sequence_index, self.info.sequence_tokens)
+
+    def cu_seqlens(self) -> np.ndarray:
+        return self._table(lib().awa_plan_cu_seqlens, self.info.window_count + 1)
+
+    def video_positions(self) -> np.ndarray:
+        return self._table(lib().awa_plan_video_positions, self.info.source_tokens)
+
+    def text_positions(self) -> np.ndarray:
+        return self._table(lib().awa_plan_text_positions, self.info.window_count * self.info.text_tokens)
+
+    def rope_table(self) -> np.ndarray:
+        return self._table(lib().awa_plan_rope_table, None, np.float32,
+                           shape=(self.info.sequence_tokens, 2 * self.info.rope_dim))
+
+    def upload(self, stream: Optional[Stream] = None) -> None:
+        check(lib().awa_plan_upload(self.h, _s(stream)), "awa_plan_upload")
+
+    # forward entry points (blobs are AwaBlob descriptors of device memory)
+    def forward(self, video_qkv: AwaBlob, text_qkv: AwaBlob, video_out: AwaBlob, text_out: AwaBlob,
+                compute: int, stream: Optional[Stream] = None) -> None:
+        check(lib().awa_forward(self.h, ctypes.byref(video_qkv), ctypes.byref(text_qkv), ctypes.byref(video_out),
+                                ctypes.byref(text_out), compute, _s(stream)), "awa_forward")
+
+    def pack(self, video_qkv: AwaBlob, text_qkv: AwaBlob, packed: AwaBlob, cu: AwaBlob,
+             stream: Optional[Stream] = None) -> None:
+        check(lib().awa_pack(self.h, ctypes.byref(video_qkv), ctypes.byref(text_qkv), ctypes.byref(packed),
+                             ctypes.byref(cu), _s(stream)), "awa_pack")
+
+    def mmrope(self, inp: AwaBlob, out: AwaBlob, stream: Optional[Stream] = None) -> None:
+        check(lib().awa_mmrope(self.h, ctypes.byref(inp), ctypes.byref(out), _s(stream)), "awa_mmrope")
+
+    def window_attention(self, inp: AwaBlob, out: AwaBlob, compute: int, stream: Optional[Stream] = None) -> None:
+        check(lib().awa_window_attention(self.h, ctypes.byref(inp), ctypes.byref(out), compute, _s(stream)),
+              "awa_window_attention")
+
+    def unpack(self, packed: AwaBlob, video_out: AwaBlob, text_out: AwaBlob, stream: Optional[Stream] = None) -> None:
+        check(lib().awa_unpack(self.h, ctypes.byref(packed), ctypes.byref(video_out), ctypes.byref(text_out),
+                               _s(stream)), "awa_unpack")
+
+
+def cast(inp: AwaBlob, out: AwaBlob, stream: Optional[Stream] = None) -> None:
+    check(lib().awa_cast(ctypes.byref(inp), ctypes.byref(out), _s(stream)), "awa_cast")
+
+
+# ---- numpy helpers for bf16 bit patterns ----
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round to nearest even, as the device does."""
+    b = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16) & 0xFFFF
+    return r.astype(np.uint16)
+
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)

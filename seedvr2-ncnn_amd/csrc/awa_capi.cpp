@@ -1,0 +1,791 @@
+// C ABI of the AWA path: runtime (memory, streams, events), plans and the
+// forward entry points. Validates every descriptor on the host and turns
+// shape errors into the reference's return codes before any kernel runs.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "awa_kernels.h"
+#include "awa_plan.h"
+#include "seedvr2_awa.h"
+
+namespace
+{
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& message)
+{
+    g_last_error = message;
+    return code;
+}
+
+int fail_hip(hipError_t e, const char* what)
+{
+    g_last_error = std::string(what) + ": " + hipGetErrorString(e);
+    return AWA_ERR_DEVICE;
+}
+
+#define HIP_TRY(expr, what)                     \
+    do                                          \
+    {                                           \
+        const hipError_t e_ = (expr);           \
+        if (e_ != hipSuccess)                   \
+            return fail_hip(e_, what);          \
+    } while (0)
+
+hipStream_t as_stream(void* s)
+{
+    return static_cast<hipStream_t>(s);
+}
+
+// ---- descriptor helpers (ncnn Mat semantics, elempack 1) ----
+
+struct QkvLayout
+{
+    int heads = 0;
+    int head_dim = 0;
+    long long token_stride = 0;
+    long long qkv_stride = 0;
+};
+
+// The four QKV layouts accepted by the reference (src/awa/awa_layers.cpp:124-170),
+// tried in the reference's order.
+bool describe_qkv(const awa_blob& b, int tokens, QkvLayout& out)
+{
+    if (!b.data || b.w <= 0 || b.h <= 0 || (b.elemsize != 2 && b.elemsize != 4))
+        return false;
+    out.head_dim = b.w;
+    if (b.dims == 3)
+    {
+        if (b.h % 3 == 0 && b.c == tokens)
+        {
+            out.heads = b.h / 3;
+            out.token_stride = b.cstep;
+            out.qkv_stride = static_cast<long long>(out.heads) * out.head_dim;
+        }
+        else if (b.c == tokens * 3)
+        {
+            out.heads = b.h;
+            out.token_stride = b.cstep;
+            out.qkv_stride = static_cast<long long>(tokens) * b.cstep;
+        }
+        else if (b.c == 3 && b.n == tokens)
+        {
+            out.heads = b.h;
+            out.token_stride = b.nstep;
+            out.qkv_stride = b.cstep;
+        }
+        else
+            return false;
+    }
+    else if (b.dims == 4)
+    {
+        if (b.d != 3 || b.c != tokens)
+            return false;
+        out.heads = b.h;
+        out.token_stride = b.cstep;
+        out.qkv_stride = static_cast<long long>(out.heads) * out.head_dim;
+    }
+    else
+        return false;
+    return out.heads > 0;
+}
+
+// Video output: Mat(d, H, N) (dims 3) or NCNN_BATCH Mat(d, H, w, h; n = t) (dims 4).
+bool describe_video_out(const awa_blob& b, const awa_plan& plan, int heads, int head_dim, awa::VideoSink& out)
+{
+    if (!b.data || (b.elemsize != 2 && b.elemsize != 4) || b.w != head_dim || b.h != heads)
+        return false;
+    out.data = b.data;
+    out.elemsize = b.elemsize;
+    if (b.dims == 3 && b.c == plan.source_tokens && b.cstep >= static_cast<long long>(heads) * head_dim)
+    {
+        out.ws = b.cstep;
+        out.hs = b.cstep * plan.source_w;
+        out.ts = b.cstep * plan.source_w * plan.source_h;
+        return true;
+    }
+    if (b.dims == 4 && b.d == plan.source_w && b.c == plan.source_h && b.n == plan.source_t)
+    {
+        out.ws = static_cast<long long>(heads) * head_dim;
+        out.hs = b.cstep;
+        out.ts = b.nstep;
+        return b.cstep >= out.ws * plan.source_w && (plan.source_t == 1 || b.nstep >= b.cstep * plan.source_h);
+    }
+    return false;
+}
+
+bool is_mat3(const awa_blob& b, int w, int h, int c)
+{
+    return b.data && b.dims == 3 && b.w == w && b.h == h && b.c == c && b.cstep >= static_cast<long long>(w) * h &&
+           (b.elemsize == 2 || b.elemsize == 4);
+}
+
+bool aligned16(const void* p)
+{
+    return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+int check_plan_uploaded(const awa_plan* plan)
+{
+    if (!plan)
+        return fail(AWA_ERR_INVALID, "null plan");
+    int device = -1;
+    if (hipGetDevice(&device) != hipSuccess)
+        return fail(AWA_ERR_DEVICE, "no HIP device");
+    if (plan->dev.device < 0)
+        return fail(AWA_ERR_INVALID, "plan has not been uploaded (awa_plan_upload)");
+    if (plan->dev.device != device)
+        return fail(AWA_ERR_INVALID, "plan was uploaded to another device");
+    return AWA_OK;
+}
+
+// Work list of the attention kernel for `heads` heads: every (window, head)
+// unit is split into query blocks of 128 rows; units are placed on the 8
+// XCDs by longest-processing-time first, and each XCD's items are laid out
+// at blockIdx = xcd + 8*j, since workgroups are dispatched round-robin over
+// the XCDs. All query blocks of one unit therefore share one XCD's L2 for
+// their K/V reads.
+constexpr int kXcds = 8;
+
+std::vector<awa::WorkItem> build_work(const awa_plan& plan, int heads)
+{
+    struct Unit
+    {
+        long long cost;
+        int window, head, qblocks;
+    };
+    std::vector<Unit> units;
+    for (size_t w = 0; w < plan.window_descs.size(); w++)
+    {
+        const int L = plan.window_descs[w].video_tokens + plan.text_tokens;
+        const int qblocks = (L + awa::kQueryRows - 1) / awa::kQueryRows;
+        for (int h = 0; h < heads; h++)
+            units.push_back({static_cast<long long>(L) * L, static_cast<int>(w), h, qblocks});
+    }
+    std::stable_sort(units.begin(), units.end(), [](const Unit& a, const Unit& b) { return a.cost > b.cost; });
+    std::vector<std::vector<awa::WorkItem>> lists(kXcds);
+    std::vector<long long> load(kXcds, 0);
+    for (const Unit& u : units)
+    {
+        const int x = static_cast<int>(std::min_element(load.begin(), load.end()) - load.begin());
+        load[x] += u.cost;
+        for (int q = 0; q < u.qblocks; q++)
+            lists[x].push_back({u.window, (u.head << 16) | q});
+    }
+    size_t longest = 0;
+    for (const auto& l : lists)
+        longest = std::max(longest, l.size());
+    std::vector<awa::WorkItem> work(longest * kXcds, awa::WorkItem{-1, 0});
+    for (int x = 0; x < kXcds; x++)
+        for (size_t j = 0; j < lists[x].size(); j++)
+            work[j * kXcds + x] = lists[x][j];
+    // Drop trailing padding.
+    while (!work.empty() && work.back().window < 0)
+        work.pop_back();
+    return work;
+}
+
+// Ensures the plan's work list for `heads` and a text-partials buffer of at
+// least `partial_bytes` exist on the device.
+int ensure_workspace(const awa_plan& plan, int heads, size_t partial_bytes)
+{
+    std::lock_guard<std::mutex> lock(plan.mutex);
+    if (plan.work_heads != heads || !plan.work)
+    {
+        const std::vector<awa::WorkItem> work = build_work(plan, heads);
+        if (plan.work)
+        {
+            (void)hipFree(plan.work);
+            plan.work = nullptr;
+        }
+        if (hipMalloc(&plan.work, std::max<size_t>(work.size(), 1) * sizeof(awa::WorkItem)) != hipSuccess)
+            return fail(AWA_ERR_ALLOC, "work list allocation failed");
+        HIP_TRY(hipMemcpy(plan.work, work.data(), work.size() * sizeof(awa::WorkItem), hipMemcpyHostToDevice),
+                "work list upload");
+        plan.work_heads = heads;
+        plan.work_count = static_cast<int>(work.size());
+    }
+    if (partial_bytes > plan.text_partials_bytes)
+    {
+        if (plan.text_partials)
+        {
+            (void)hipFree(plan.text_partials);
+            plan.text_partials = nullptr;
+            plan.text_partials_bytes = 0;
+        }
+        if (hipMalloc(&plan.text_partials, partial_bytes) != hipSuccess)
+            return fail(AWA_ERR_ALLOC, "text partial workspace allocation failed");
+        plan.text_partials_bytes = partial_bytes;
+    }
+    return AWA_OK;
+}
+
+template <typename T>
+int upload_vector(T*& dst, const std::vector<T>& src, hipStream_t stream)
+{
+    if (dst)
+    {
+        (void)hipFree(dst);
+        dst = nullptr;
+    }
+    const size_t bytes = std::max<size_t>(src.size(), 1) * sizeof(T);
+    if (hipMalloc(&dst, bytes) != hipSuccess)
+        return fail(AWA_ERR_ALLOC, "plan table allocation failed");
+    if (!src.empty())
+        HIP_TRY(hipMemcpyAsync(dst, src.data(), src.size() * sizeof(T), hipMemcpyHostToDevice, stream), "plan upload");
+    return AWA_OK;
+}
+
+void free_device(awa_plan& plan)
+{
+    auto release = [](auto*& p) {
+        if (p)
+            (void)hipFree(p);
+        p = nullptr;
+    };
+    release(plan.dev.windows);
+    release(plan.dev.rows);
+    release(plan.dev.video_positions);
+    release(plan.dev.text_positions);
+    release(plan.dev.cu_seqlens);
+    release(plan.dev.rope_cs);
+    release(plan.work);
+    release(plan.text_partials);
+    plan.text_partials_bytes = 0;
+    plan.work_heads = 0;
+    plan.work_count = 0;
+    plan.dev.device = -1;
+}
+
+} // namespace
+
+extern "C" {
+
+const char* awa_last_error(void)
+{
+    return g_last_error.c_str();
+}
+
+int awa_device_count(int* count)
+{
+    if (!count)
+        return fail(AWA_ERR_INVALID, "null count");
+    int n = 0;
+    const hipError_t e = hipGetDeviceCount(&n);
+    *count = e == hipSuccess ? n : 0;
+    return AWA_OK;
+}
+
+int awa_runtime_init(int device)
+{
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+        return fail(AWA_ERR_DEVICE, "no HIP device available");
+    if (device < 0 || device >= n)
+        return fail(AWA_ERR_INVALID, "device index out of range");
+    HIP_TRY(hipSetDevice(device), "hipSetDevice");
+    return AWA_OK;
+}
+
+int awa_malloc(void** ptr, size_t bytes)
+{
+    if (!ptr)
+        return fail(AWA_ERR_INVALID, "null pointer");
+    *ptr = nullptr;
+    if (bytes == 0)
+        return AWA_OK;
+    if (hipMalloc(ptr, bytes) != hipSuccess)
+    {
+        *ptr = nullptr;
+        return fail(AWA_ERR_ALLOC, "device allocation failed");
+    }
+    return AWA_OK;
+}
+
+int awa_free(void* ptr)
+{
+    if (ptr)
+        HIP_TRY(hipFree(ptr), "hipFree");
+    return AWA_OK;
+}
+
+int awa_host_alloc(void** ptr, size_t bytes)
+{
+    if (!ptr)
+        return fail(AWA_ERR_INVALID, "null pointer");
+    *ptr = nullptr;
+    if (bytes == 0)
+        return AWA_OK;
+    if (hipHostMalloc(ptr, bytes, hipHostMallocDefault) != hipSuccess)
+    {
+        *ptr = nullptr;
+        return fail(AWA_ERR_ALLOC, "pinned host allocation failed");
+    }
+    return AWA_OK;
+}
+
+int awa_host_free(void* ptr)
+{
+    if (ptr)
+        HIP_TRY(hipHostFree(ptr), "hipHostFree");
+    return AWA_OK;
+}
+
+int awa_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream)
+{
+    if (bytes && (!dst || !src))
+        return fail(AWA_ERR_INVALID, "null pointer");
+    if (bytes)
+        HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, as_stream(stream)), "copy to device");
+    return AWA_OK;
+}
+
+int awa_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream)
+{
+    if (bytes && (!dst || !src))
+        return fail(AWA_ERR_INVALID, "null pointer");
+    if (bytes)
+        HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, as_stream(stream)), "copy to host");
+    return AWA_OK;
+}
+
+int awa_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream)
+{
+    if (bytes && (!dst || !src))
+        return fail(AWA_ERR_INVALID, "null pointer");
+    if (bytes)
+        HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream)), "device copy");
+    return AWA_OK;
+}
+
+int awa_zero(void* dst, size_t bytes, void* stream)
+{
+    if (bytes && !dst)
+        return fail(AWA_ERR_INVALID, "null pointer");
+    HIP_TRY(awa::launch_zero(dst, bytes, as_stream(stream)), "zero kernel");
+    return AWA_OK;
+}
+
+int awa_stream_create(void** stream)
+{
+    if (!stream)
+        return fail(AWA_ERR_INVALID, "null pointer");
+    hipStream_t s = nullptr;
+    HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+    *stream = s;
+    return AWA_OK;
+}
+
+int awa_stream_destroy(void* stream)
+{
+    if (stream)
+        HIP_TRY(hipStreamDestroy(as_stream(stream)), "hipStreamDestroy");
+    return AWA_OK;
+}
+
+int awa_stream_synchronize(void* stream)
+{
+    HIP_TRY(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize");
+    return AWA_OK;
+}
+
+int awa_event_create(void** event)
+{
+    if (!event)
+        return fail(AWA_ERR_INVALID, "null pointer");
+    hipEvent_t e = nullptr;
+    HIP_TRY(hipEventCreate(&e), "hipEventCreate");
+    *event = e;
+    return AWA_OK;
+}
+
+int awa_event_destroy(void* event)
+{
+    if (event)
+        HIP_TRY(hipEventDestroy(static_cast<hipEvent_t>(event)), "hipEventDestroy");
+    return AWA_OK;
+}
+
+int awa_event_record(void* event, void* stream)
+{
+    if (!event)
+        return fail(AWA_ERR_INVALID, "null event");
+    HIP_TRY(hipEventRecord(static_cast<hipEvent_t>(event), as_stream(stream)), "hipEventRecord");
+    return AWA_OK;
+}
+
+int awa_event_synchronize(void* event)
+{
+    if (!event)
+        return fail(AWA_ERR_INVALID, "null event");
+    HIP_TRY(hipEventSynchronize(static_cast<hipEvent_t>(event)), "hipEventSynchronize");
+    return AWA_OK;
+}
+
+int awa_event_elapsed_ms(void* start, void* stop, float* ms)
+{
+    if (!start || !stop || !ms)
+        return fail(AWA_ERR_INVALID, "null argument");
+    HIP_TRY(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)),
+            "hipEventElapsedTime");
+    return AWA_OK;
+}
+
+int awa_fill_normal(void* dst, size_t count, int elemsize, unsigned long long seed, void* stream)
+{
+    if ((count && !dst) || (elemsize != 2 && elemsize != 4))
+        return fail(AWA_ERR_INVALID, "invalid fill arguments");
+    if (count)
+        HIP_TRY(awa::launch_fill_normal(dst, count, elemsize, seed, as_stream(stream)), "fill kernel");
+    return AWA_OK;
+}
+
+// ---- plans ----
+
+int awa_plan_create(const awa_plan_desc* desc, awa_plan** plan)
+{
+    if (!desc || !plan)
+        return fail(AWA_ERR_INVALID, "null argument");
+    *plan = nullptr;
+    awa_plan* p = new (std::nothrow) awa_plan();
+    if (!p)
+        return fail(AWA_ERR_ALLOC, "plan allocation failed");
+    std::string error;
+    const int rc = awa::build_plan(*desc, *p, error);
+    if (rc != AWA_OK)
+    {
+        delete p;
+        return fail(rc, error);
+    }
+    *plan = p;
+    return AWA_OK;
+}
+
+void awa_plan_destroy(awa_plan* plan)
+{
+    if (!plan)
+        return;
+    if (plan->dev.device >= 0)
+    {
+        int current = -1;
+        (void)hipGetDevice(&current);
+        (void)hipSetDevice(plan->dev.device);
+        free_device(*plan);
+        if (current >= 0)
+            (void)hipSetDevice(current);
+    }
+    delete plan;
+}
+
+int awa_plan_info_get(const awa_plan* plan, awa_plan_info* info)
+{
+    if (!plan || !info)
+        return fail(AWA_ERR_INVALID, "null argument");
+    info->source_t = plan->source_t;
+    info->source_h = plan->source_h;
+    info->source_w = plan->source_w;
+    info->source_tokens = plan->source_tokens;
+    info->text_tokens = plan->text_tokens;
+    info->window_count = static_cast<int>(plan->windows.size());
+    info->sequence_tokens = plan->sequence_tokens;
+    info->window_t = plan->window_t;
+    info->window_h = plan->window_h;
+    info->window_w = plan->window_w;
+    info->max_window_tokens = plan->max_window_tokens;
+    info->rope_dim = plan->rope_dim;
+    info->shifted = plan->shifted ? 1 : 0;
+    return AWA_OK;
+}
+
+int awa_plan_windows(const awa_plan* plan, int* out)
+{
+    if (!plan || !out)
+        return fail(AWA_ERR_INVALID, "null argument");
+    for (size_t i = 0; i < plan->windows.size(); i++)
+    {
+        const awa::Box& b = plan->windows[i];
+        const int v[6] = {b.t0, b.t1, b.h0, b.h1, b.w0, b.w1};
+        std::memcpy(out + 6 * i, v, sizeof(v));
+    }
+    return AWA_OK;
+}
+
+#define COPY_TABLE(fn, field)                                                        \
+    int fn(const awa_plan* plan, int* out)                                           \
+    {                                                                                \
+        if (!plan || !out)                                                           \
+            return fail(AWA_ERR_INVALID, "null argument");                           \
+        std::memcpy(out, plan->field.data(), plan->field.size() * sizeof(int));      \
+        return AWA_OK;                                                               \
+    }
+
+COPY_TABLE(awa_plan_sequence_index, sequence_index)
+COPY_TABLE(awa_plan_cu_seqlens, cu_seqlens)
+COPY_TABLE(awa_plan_video_positions, video_positions)
+COPY_TABLE(awa_plan_text_positions, text_positions)
+
+int awa_plan_rope_table(const awa_plan* plan, float* out)
+{
+    if (!plan || !out)
+        return fail(AWA_ERR_INVALID, "null argument");
+    for (int p = 0; p < plan->sequence_tokens; p++)
+        awa::rope_row(*plan, p, out + static_cast<size_t>(p) * 2 * plan->rope_dim);
+    return AWA_OK;
+}
+
+int awa_plan_upload(awa_plan* plan, void* stream)
+{
+    if (!plan)
+        return fail(AWA_ERR_INVALID, "null plan");
+    int device = -1;
+    HIP_TRY(hipGetDevice(&device), "hipGetDevice");
+    std::lock_guard<std::mutex> lock(plan->mutex);
+    if (plan->dev.device >= 0 && plan->dev.device != device)
+        return fail(AWA_ERR_INVALID, "plan already uploaded to another device");
+    hipStream_t s = as_stream(stream);
+    int rc;
+    if ((rc = upload_vector(plan->dev.windows, plan->window_descs, s)) != AWA_OK ||
+        (rc = upload_vector(plan->dev.rows, plan->rows, s)) != AWA_OK ||
+        (rc = upload_vector(plan->dev.video_positions, plan->video_positions, s)) != AWA_OK ||
+        (rc = upload_vector(plan->dev.text_positions, plan->text_positions, s)) != AWA_OK ||
+        (rc = upload_vector(plan->dev.cu_seqlens, plan->cu_seqlens, s)) != AWA_OK ||
+        (rc = upload_vector(plan->dev.rope_cs, plan->rope_cs, s)) != AWA_OK)
+        return rc;
+    HIP_TRY(hipStreamSynchronize(s), "plan upload sync");
+    plan->dev.device = device;
+    return AWA_OK;
+}
+
+// ---- forward ----
+
+int awa_forward(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv, const awa_blob* video_out,
+                const awa_blob* text_out, int compute, void* stream)
+{
+    int rc = check_plan_uploaded(plan);
+    if (rc != AWA_OK)
+        return rc;
+    if (!video_qkv || !text_qkv || !video_out || !text_out)
+        return fail(AWA_ERR_INVALID, "null blob");
+    if (compute != AWA_COMPUTE_F32 && compute != AWA_COMPUTE_BF16)
+        return fail(AWA_ERR_INVALID, "unknown compute mode");
+    QkvLayout vl, tl;
+    if (!describe_qkv(*video_qkv, plan->source_tokens, vl) || !describe_qkv(*text_qkv, plan->text_tokens, tl) ||
+        vl.heads != tl.heads || vl.head_dim != tl.head_dim || video_qkv->elemsize != text_qkv->elemsize)
+        return fail(AWA_ERR_INVALID, "invalid QKV input blobs");
+    if (vl.head_dim != awa::kHeadDim || plan->rope_dim != awa::kRopeDim)
+        return fail(AWA_ERR_INVALID, "fused path needs head_dim 128 and rope_dim 126; use the staged entry points");
+    if (plan->rope_coords > awa::kMaxRopeCoords)
+        return fail(AWA_ERR_INVALID, "RoPE coordinate range exceeds the fused kernel's table");
+    const int elem = video_qkv->elemsize;
+    const int align_elems = 16 / elem;
+    if (!aligned16(video_qkv->data) || !aligned16(text_qkv->data) || vl.token_stride % align_elems ||
+        vl.qkv_stride % align_elems || tl.token_stride % align_elems || tl.qkv_stride % align_elems)
+        return fail(AWA_ERR_INVALID, "QKV blobs must be 16-byte aligned with 16-byte aligned strides");
+    awa::VideoSink sink{};
+    if (!describe_video_out(*video_out, *plan, vl.heads, vl.head_dim, sink))
+        return fail(AWA_ERR_INVALID, "invalid video output blob");
+    if (!is_mat3(*text_out, vl.head_dim, vl.heads, plan->text_tokens))
+        return fail(AWA_ERR_INVALID, "invalid text output blob");
+    const int out_align = 16 / video_out->elemsize;
+    if (!aligned16(video_out->data) || sink.ts % out_align || sink.hs % out_align || sink.ws % out_align ||
+        !aligned16(text_out->data) || text_out->cstep % (16 / text_out->elemsize))
+        return fail(AWA_ERR_INVALID, "output blobs must be 16-byte aligned with 16-byte aligned strides");
+
+    const size_t partial_bytes = plan->windows.size() * static_cast<size_t>(plan->text_tokens) * vl.heads *
+                                 vl.head_dim * sizeof(float);
+    if ((rc = ensure_workspace(*plan, vl.heads, partial_bytes)) != AWA_OK)
+        return rc;
+
+    awa::AttentionLaunch p{};
+    p.fused = true;
+    p.bf16_mfma = compute == AWA_COMPUTE_BF16;
+    p.video = {video_qkv->data, vl.token_stride, vl.qkv_stride, elem};
+    p.text = {text_qkv->data, tl.token_stride, tl.qkv_stride, elem};
+    p.video_out = sink;
+    p.text_partials = plan->text_partials;
+    p.windows = plan->dev.windows;
+    p.work = plan->work;
+    p.work_count = plan->work_count;
+    p.rope_cs = plan->dev.rope_cs;
+    p.rope_coords = plan->rope_coords;
+    p.heads = vl.heads;
+    p.text_tokens = plan->text_tokens;
+    p.source_h = plan->source_h;
+    p.source_w = plan->source_w;
+    p.scale_log2 = (1.f / std::sqrt(static_cast<float>(vl.head_dim))) * 1.4426950408889634f;
+    hipStream_t s = as_stream(stream);
+    HIP_TRY(awa::launch_attention(p, s), "attention kernel launch");
+    HIP_TRY(awa::launch_text_mean(plan->text_partials, static_cast<int>(plan->windows.size()), plan->text_tokens,
+                                  vl.heads, vl.head_dim, text_out->data, text_out->cstep, text_out->elemsize, s),
+            "text mean kernel launch");
+    return AWA_OK;
+}
+
+int awa_pack(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv, const awa_blob* packed,
+             const awa_blob* cu_seqlens, void* stream)
+{
+    int rc = check_plan_uploaded(plan);
+    if (rc != AWA_OK)
+        return rc;
+    if (!video_qkv || !text_qkv || !packed || !cu_seqlens)
+        return fail(AWA_ERR_INVALID, "null blob");
+    QkvLayout vl, tl;
+    if (!describe_qkv(*video_qkv, plan->source_tokens, vl) || !describe_qkv(*text_qkv, plan->text_tokens, tl) ||
+        vl.heads != tl.heads || vl.head_dim != tl.head_dim)
+        return fail(AWA_ERR_INVALID, "invalid QKV input blobs");
+    if (!is_mat3(*packed, vl.head_dim, 3 * vl.heads, plan->sequence_tokens) || packed->elemsize != 4)
+        return fail(AWA_ERR_INVALID, "packed output must be fp32 Mat(d, 3H, S)");
+    const int cu_count = static_cast<int>(plan->cu_seqlens.size());
+    if (!cu_seqlens->data || cu_seqlens->dims != 1 || cu_seqlens->w != cu_count || cu_seqlens->elemsize != 4)
+        return fail(AWA_ERR_INVALID, "cu_seqlens output must be fp32 Mat(nwin+1)");
+    hipStream_t s = as_stream(stream);
+    const awa::QkvSource vs{video_qkv->data, vl.token_stride, vl.qkv_stride, video_qkv->elemsize};
+    const awa::QkvSource ts{text_qkv->data, tl.token_stride, tl.qkv_stride, text_qkv->elemsize};
+    HIP_TRY(awa::launch_pack(plan->dev.rows, plan->sequence_tokens, plan->source_tokens, vs, ts, vl.heads,
+                             vl.head_dim, static_cast<float*>(packed->data), packed->cstep, s),
+            "pack kernel launch");
+    HIP_TRY(awa::launch_cu_seqlens(plan->dev.cu_seqlens, cu_count, static_cast<float*>(cu_seqlens->data), s),
+            "cu_seqlens kernel launch");
+    return AWA_OK;
+}
+
+int awa_mmrope(const awa_plan* plan, const awa_blob* input, const awa_blob* output, void* stream)
+{
+    int rc = check_plan_uploaded(plan);
+    if (rc != AWA_OK)
+        return rc;
+    if (!input || !output)
+        return fail(AWA_ERR_INVALID, "null blob");
+    // src/awa/awa_layers.cpp:997-1004: w >= rope_dim, h % 3 == 0, c == S.
+    if (!input->data || input->dims != 3 || input->w < plan->rope_dim || input->h <= 0 || input->h % 3 != 0 ||
+        input->c != plan->sequence_tokens || (input->elemsize != 2 && input->elemsize != 4))
+        return fail(AWA_ERR_INVALID, "invalid MMRoPE input");
+    if (!is_mat3(*output, input->w, input->h, input->c) || output->elemsize != 4)
+        return fail(AWA_ERR_INVALID, "MMRoPE output must be fp32 with the input's shape");
+    const int heads = input->h / 3;
+    HIP_TRY(awa::launch_mmrope(plan->dev.rows, plan->sequence_tokens, input->data, input->cstep, input->elemsize,
+                               static_cast<float*>(output->data), output->cstep, heads, input->w, plan->rope_dim,
+                               plan->rope_pairs, plan->dev.rope_cs, as_stream(stream)),
+            "MMRoPE kernel launch");
+    return AWA_OK;
+}
+
+int awa_window_attention(const awa_plan* plan, const awa_blob* input, const awa_blob* output, int compute,
+                         void* stream)
+{
+    int rc = check_plan_uploaded(plan);
+    if (rc != AWA_OK)
+        return rc;
+    if (!input || !output)
+        return fail(AWA_ERR_INVALID, "null blob");
+    if (compute != AWA_COMPUTE_F32 && compute != AWA_COMPUTE_BF16)
+        return fail(AWA_ERR_INVALID, "unknown compute mode");
+    if (!input->data || input->dims != 3 || input->w <= 0 || input->h <= 0 || input->h % 3 != 0 ||
+        input->c != plan->sequence_tokens || (input->elemsize != 2 && input->elemsize != 4))
+        return fail(AWA_ERR_INVALID, "invalid WindowAttention input");
+    const int heads = input->h / 3;
+    const int head_dim = input->w;
+    if (!is_mat3(*output, head_dim, heads, plan->sequence_tokens) || output->elemsize != 4)
+        return fail(AWA_ERR_INVALID, "WindowAttention output must be fp32 Mat(d, H, S)");
+    hipStream_t s = as_stream(stream);
+    if (head_dim != awa::kHeadDim)
+    {
+        if (head_dim > 1024)
+            return fail(AWA_ERR_INVALID, "head_dim above 1024 is not supported");
+        HIP_TRY(awa::launch_attention_generic(input->data, input->cstep, input->elemsize,
+                                              static_cast<float*>(output->data), output->cstep, plan->dev.cu_seqlens,
+                                              static_cast<int>(plan->windows.size()), heads, head_dim,
+                                              plan->sequence_tokens, s),
+                "generic attention kernel launch");
+        return AWA_OK;
+    }
+    const int align_elems = 16 / input->elemsize;
+    if (!aligned16(input->data) || input->cstep % align_elems || !aligned16(output->data) || output->cstep % 4)
+        return fail(AWA_ERR_INVALID, "packed blobs must be 16-byte aligned with 16-byte aligned strides");
+    if ((rc = ensure_workspace(*plan, heads, 0)) != AWA_OK)
+        return rc;
+    awa::AttentionLaunch p{};
+    p.fused = false;
+    p.bf16_mfma = compute == AWA_COMPUTE_BF16;
+    p.packed_in = input->data;
+    p.packed_in_row = input->cstep;
+    p.packed_in_elemsize = input->elemsize;
+    p.packed_out = static_cast<float*>(output->data);
+    p.packed_out_row = output->cstep;
+    p.windows = plan->dev.windows;
+    p.work = plan->work;
+    p.work_count = plan->work_count;
+    p.heads = heads;
+    p.text_tokens = plan->text_tokens;
+    p.source_h = plan->source_h;
+    p.source_w = plan->source_w;
+    p.scale_log2 = (1.f / std::sqrt(static_cast<float>(head_dim))) * 1.4426950408889634f;
+    HIP_TRY(awa::launch_attention(p, s), "attention kernel launch");
+    return AWA_OK;
+}
+
+int awa_unpack(const awa_plan* plan, const awa_blob* packed, const awa_blob* video_out, const awa_blob* text_out,
+               void* stream)
+{
+    int rc = check_plan_uploaded(plan);
+    if (rc != AWA_OK)
+        return rc;
+    if (!packed || !video_out || !text_out)
+        return fail(AWA_ERR_INVALID, "null blob");
+    // src/awa/awa_layers.cpp:755-762
+    if (!packed->data || packed->dims != 3 || packed->w <= 0 || packed->h <= 0 ||
+        packed->c != plan->sequence_tokens || (packed->elemsize != 2 && packed->elemsize != 4))
+        return fail(AWA_ERR_INVALID, "invalid packed input");
+    const int heads = packed->h;
+    const int head_dim = packed->w;
+    awa::VideoSink sink{};
+    if (!describe_video_out(*video_out, *plan, heads, head_dim, sink))
+        return fail(AWA_ERR_INVALID, "invalid video output blob");
+    if (!is_mat3(*text_out, head_dim, heads, plan->text_tokens))
+        return fail(AWA_ERR_INVALID, "invalid text output blob");
+    hipStream_t s = as_stream(stream);
+    HIP_TRY(awa::launch_unpack_video(plan->dev.video_positions, plan->source_t, plan->source_h, plan->source_w,
+                                     packed->data, packed->cstep, packed->elemsize, sink, heads, head_dim, s),
+            "unpack video kernel launch");
+    HIP_TRY(awa::launch_unpack_text(plan->dev.text_positions, static_cast<int>(plan->windows.size()),
+                                    plan->text_tokens, packed->data, packed->cstep, packed->elemsize, text_out->data,
+                                    text_out->cstep, text_out->elemsize, heads, head_dim, s),
+            "unpack text kernel launch");
+    return AWA_OK;
+}
+
+int awa_cast(const awa_blob* input, const awa_blob* output, void* stream)
+{
+    if (!input || !output || !input->data || !output->data)
+        return fail(AWA_ERR_INVALID, "null blob");
+    if ((input->elemsize != 2 && input->elemsize != 4) || (output->elemsize != 2 && output->elemsize != 4))
+        return fail(AWA_ERR_INVALID, "cast supports fp32 and bf16");
+    if (input->dims != output->dims || input->w != output->w || input->h != output->h || input->d != output->d ||
+        input->c != output->c || input->n != output->n || input->dims < 1 || input->dims > 4 || input->n < 1)
+        return fail(AWA_ERR_INVALID, "cast needs blobs of one shape");
+    awa::CastShape s{};
+    s.w = input->w;
+    s.h = input->dims >= 2 ? input->h : 1;
+    s.d = input->dims == 4 ? input->d : 1;
+    s.c = input->dims >= 3 ? input->c : 1;
+    s.n = input->n;
+    // Elements of one channel are dense; channels and batches are strided.
+    const long long plane = static_cast<long long>(s.w) * s.h * s.d;
+    s.in_cstep = input->dims >= 3 ? input->cstep : plane;
+    s.out_cstep = output->dims >= 3 ? output->cstep : plane;
+    s.in_nstep = input->n > 1 ? input->nstep : s.in_cstep * s.c;
+    s.out_nstep = output->n > 1 ? output->nstep : s.out_cstep * s.c;
+    HIP_TRY(awa::launch_cast(input->data, input->elemsize, output->data, output->elemsize, s, as_stream(stream)),
+            "cast kernel launch");
+    return AWA_OK;
+}
+
+} // extern "C"

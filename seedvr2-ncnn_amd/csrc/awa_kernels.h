@@ -1,0 +1,104 @@
+// Launch interface of the AWA HIP kernels (gfx950). All pointers are device
+// pointers; strides are in elements.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "awa_plan.h"
+
+namespace awa
+{
+
+constexpr int kHeadDim = 128;   // head_dim of the MFMA attention kernels
+constexpr int kRopeDim = 126;   // rope_dim of the fused kernel
+constexpr int kQueryRows = 128; // query rows per workgroup (4 waves x 32)
+constexpr int kMaxRopeCoords = 128; // RoPE coordinates the fused kernel holds in LDS
+
+// One QKV source: row of (token, qkv, head) starts at
+// token * token_stride + qkv * qkv_stride + head * head_dim.
+struct QkvSource
+{
+    const void* data;
+    long long token_stride;
+    long long qkv_stride;
+    int elemsize;
+};
+
+// Video output addressing: token (t, h, w) starts at t*ts + h*hs + w*ws.
+struct VideoSink
+{
+    void* data;
+    long long ts, hs, ws;
+    int elemsize;
+};
+
+struct AttentionLaunch
+{
+    bool fused;      // gather + RoPE from video/text sources, scatter to video/text
+    bool bf16_mfma;  // AWA_COMPUTE_BF16
+    // fused inputs / outputs
+    QkvSource video, text;
+    VideoSink video_out;
+    float* text_partials; // [nwin][T_x][H][d] fp32
+    // packed inputs / outputs (fused == false)
+    const void* packed_in;
+    long long packed_in_row;
+    int packed_in_elemsize;
+    float* packed_out;
+    long long packed_out_row;
+    // geometry
+    const WindowDesc* windows;
+    const WorkItem* work;
+    int work_count;
+    const float* rope_cs;
+    int rope_coords;
+    int heads;
+    int text_tokens;
+    int source_h, source_w;
+    float scale_log2; // (1/sqrt(head_dim)) * log2(e)
+};
+
+hipError_t launch_attention(const AttentionLaunch& p, hipStream_t stream);
+
+// text_out[k][head][:] = (sum_w partials[w][k][head][:]) / nwin, window order.
+hipError_t launch_text_mean(const float* partials, int window_count, int text_tokens, int heads, int head_dim,
+                            void* text_out, long long text_token_stride, int out_elemsize, hipStream_t stream);
+
+// Generic (head_dim <= 1024) window attention over a packed [S][3H][d] blob;
+// used by the staged entry point when head_dim != 128.
+hipError_t launch_attention_generic(const void* packed_in, long long in_row, int in_elemsize, float* out,
+                                    long long out_row, const int* cu_seqlens_dev, int window_count, int heads,
+                                    int head_dim, int sequence_tokens, hipStream_t stream);
+
+hipError_t launch_pack(const RowInfo* rows, int sequence_tokens, int source_tokens, const QkvSource& video,
+                       const QkvSource& text, int heads, int head_dim, float* packed, long long packed_row,
+                       hipStream_t stream);
+
+hipError_t launch_cu_seqlens(const int* cu_dev, int count, float* out, hipStream_t stream);
+
+hipError_t launch_mmrope(const RowInfo* rows, int sequence_tokens, const void* in, long long in_row,
+                         int in_elemsize, float* out, long long out_row, int heads, int head_dim, int rope_dim,
+                         int rope_pairs, const float* rope_cs, hipStream_t stream);
+
+hipError_t launch_unpack_video(const int* video_positions, int source_t, int source_h, int source_w,
+                               const void* packed, long long packed_row, int packed_elemsize, const VideoSink& out,
+                               int heads, int head_dim, hipStream_t stream);
+
+hipError_t launch_unpack_text(const int* text_positions, int window_count, int text_tokens, const void* packed,
+                              long long packed_row, int packed_elemsize, void* out, long long out_row,
+                              int out_elemsize, int heads, int head_dim, hipStream_t stream);
+
+// Strided element cast between fp32 and bf16 (or same-type copy): element
+// (x, y, z, c, b) at b*nstep + c*cstep + (z*h + y)*w + x on both sides.
+struct CastShape
+{
+    int w, h, d, c, n;
+    long long in_cstep, in_nstep, out_cstep, out_nstep;
+};
+hipError_t launch_cast(const void* in, int in_elemsize, void* out, int out_elemsize, const CastShape& s,
+                       hipStream_t stream);
+
+hipError_t launch_fill_normal(void* dst, size_t count, int elemsize, unsigned long long seed, hipStream_t stream);
+hipError_t launch_zero(void* dst, size_t bytes, hipStream_t stream);
+
+} // namespace awa

@@ -1,0 +1,416 @@
+// Data-movement kernels of the AWA path (gfx950): the staged Pack, MMRoPE and
+// Unpack layers, the ordered text mean of the fused path, a generic-head_dim
+// window attention for the staged layer, casts, fills.
+//
+// All of these are HBM-bound byte movers: each thread moves 4 consecutive
+// elements (16 B of fp32 / 8 B of bf16) so that a wave touches contiguous
+// 256-1024 B runs of a row.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "awa_kernels.h"
+
+namespace awa
+{
+namespace
+{
+
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b)
+{
+    return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f)
+{
+    const uint32_t bits = __float_as_uint(f);
+    return static_cast<uint16_t>((bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16);
+}
+
+__device__ __forceinline__ float load_elem(const void* base, long long index, int elemsize)
+{
+    return elemsize == 4 ? static_cast<const float*>(base)[index]
+                         : bf16_to_f32(static_cast<const uint16_t*>(base)[index]);
+}
+
+__device__ __forceinline__ void store_elem(void* base, long long index, int elemsize, float v)
+{
+    if (elemsize == 4)
+        static_cast<float*>(base)[index] = v;
+    else
+        static_cast<uint16_t*>(base)[index] = f32_to_bf16(v);
+}
+
+// ---- Pack: packed[p][qkv][head][f] = source row (src/awa/awa_layers.cpp:440-454) ----
+__global__ void pack_kernel(const RowInfo* rows, int sequence_tokens, int source_tokens, QkvSource video,
+                            QkvSource text, int heads, int head_dim, float* packed, long long packed_row)
+{
+    const int row_elems = 3 * heads * head_dim;
+    const long long total = static_cast<long long>(sequence_tokens) * row_elems;
+    const long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= total)
+        return;
+    const int position = static_cast<int>(idx / row_elems);
+    const int e = static_cast<int>(idx - static_cast<long long>(position) * row_elems);
+    const int qkv = e / (heads * head_dim);
+    const int rest = e - qkv * heads * head_dim;
+    const int source = rows[position].source;
+    const bool is_video = source < source_tokens;
+    const QkvSource& src = is_video ? video : text;
+    const long long token = is_video ? source : source - source_tokens;
+    packed[position * packed_row + e] =
+        load_elem(src.data, token * src.token_stride + qkv * src.qkv_stride + rest, src.elemsize);
+}
+
+__global__ void cu_seqlens_kernel(const int* cu, int count, float* out)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count)
+        out[i] = static_cast<float>(cu[i]);
+}
+
+// ---- MMRoPE on a packed blob (src/awa/awa_layers.cpp:930-951): one thread per feature pair ----
+__global__ void mmrope_kernel(const RowInfo* rows, int sequence_tokens, const void* in, long long in_row,
+                              int in_elemsize, float* out, long long out_row, int heads, int head_dim, int rope_dim,
+                              int rope_pairs, const float* rope_cs)
+{
+#pragma clang fp contract(off)
+    const int pairs_per_row = 3 * heads * head_dim / 2;
+    const long long total = static_cast<long long>(sequence_tokens) * pairs_per_row;
+    const long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= total)
+        return;
+    const int position = static_cast<int>(idx / pairs_per_row);
+    const int pair_in_row = static_cast<int>(idx - static_cast<long long>(position) * pairs_per_row);
+    const int e = 2 * pair_in_row; // even element index within the row
+    const int qkv_head = e / head_dim;
+    const int feature = e - qkv_head * head_dim;
+    const long long src = position * in_row + e;
+    const long long dst = position * out_row + e;
+    float x0 = load_elem(in, src, in_elemsize);
+    float x1;
+    if (feature + 1 < head_dim)
+        x1 = load_elem(in, src + 1, in_elemsize);
+    else
+        x1 = 0.f;
+    if (qkv_head < 2 * heads && feature < rope_dim)
+    {
+        // rope_dim is even, so feature+1 < rope_dim too.
+        const RowInfo r = rows[position];
+        const int pair = feature >> 1;
+        const int axis = pair / rope_pairs;
+        const int pp = pair - axis * rope_pairs;
+        const int coord = axis == 0 ? r.ct : (axis == 1 ? r.ch : r.cw);
+        const float c = rope_cs[(coord * rope_pairs + pp) * 2];
+        const float s = rope_cs[(coord * rope_pairs + pp) * 2 + 1];
+        const float y0 = x0 * c - x1 * s;
+        const float y1 = x1 * c + x0 * s;
+        x0 = y0;
+        x1 = y1;
+    }
+    out[dst] = x0;
+    if (feature + 1 < head_dim)
+        out[dst + 1] = x1;
+}
+
+// ---- Unpack video: video[t][h][w][head][f] = packed[video_positions[token]] (awa_layers.cpp:659-676) ----
+__global__ void unpack_video_kernel(const int* video_positions, int source_t, int source_h, int source_w,
+                                    const void* packed, long long packed_row, int packed_elemsize, VideoSink out,
+                                    int row_elems)
+{
+    const long long total = static_cast<long long>(source_t) * source_h * source_w * row_elems;
+    const long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= total)
+        return;
+    const int token = static_cast<int>(idx / row_elems);
+    const int e = static_cast<int>(idx - static_cast<long long>(token) * row_elems);
+    const int t = token / (source_h * source_w);
+    const int spatial = token - t * source_h * source_w;
+    const int h = spatial / source_w;
+    const int w = spatial - h * source_w;
+    const float v = load_elem(packed, video_positions[token] * packed_row + e, packed_elemsize);
+    store_elem(out.data, t * out.ts + h * out.hs + w * out.ws + e, out.elemsize, v);
+}
+
+// ---- Unpack text: (sum over windows in window order) / nwin (src/awa/shader/awa_unpack.comp:47-58) ----
+__global__ void unpack_text_kernel(const int* text_positions, int window_count, int text_tokens, const void* packed,
+                                   long long packed_row, int packed_elemsize, void* out, long long out_row,
+                                   int out_elemsize, int row_elems)
+{
+    const long long total = static_cast<long long>(text_tokens) * row_elems;
+    const long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= total)
+        return;
+    const int k = static_cast<int>(idx / row_elems);
+    const int e = static_cast<int>(idx - static_cast<long long>(k) * row_elems);
+    float sum = 0.f;
+    for (int w = 0; w < window_count; w++)
+        sum += load_elem(packed, text_positions[w * text_tokens + k] * packed_row + e, packed_elemsize);
+    store_elem(out, k * out_row + e, out_elemsize, sum / static_cast<float>(window_count));
+}
+
+// ---- Fused-path text mean over the per-window partials [nwin][T_x][H][d] ----
+__global__ void text_mean_kernel(const float* partials, int window_count, int text_tokens, int row_elems,
+                                 void* out, long long out_row, int out_elemsize)
+{
+    const int groups = row_elems / 4;
+    const long long total = static_cast<long long>(text_tokens) * groups;
+    const long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= total)
+        return;
+    const int k = static_cast<int>(idx / groups);
+    const int e = 4 * static_cast<int>(idx - static_cast<long long>(k) * groups);
+    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+    const long long window_stride = static_cast<long long>(text_tokens) * row_elems;
+    const float* src = partials + static_cast<long long>(k) * row_elems + e;
+    for (int w = 0; w < window_count; w++)
+    {
+        const float4 v = *reinterpret_cast<const float4*>(src + w * window_stride);
+        sum.x += v.x;
+        sum.y += v.y;
+        sum.z += v.z;
+        sum.w += v.w;
+    }
+    const float n = static_cast<float>(window_count);
+    const long long o = k * out_row + e;
+    if (out_elemsize == 4)
+    {
+        *reinterpret_cast<float4*>(static_cast<float*>(out) + o) = make_float4(sum.x / n, sum.y / n, sum.z / n, sum.w / n);
+    }
+    else
+    {
+        uint16_t* dst = static_cast<uint16_t*>(out) + o;
+        const uint32_t lo = f32_to_bf16(sum.x / n) | (static_cast<uint32_t>(f32_to_bf16(sum.y / n)) << 16);
+        const uint32_t hi = f32_to_bf16(sum.z / n) | (static_cast<uint32_t>(f32_to_bf16(sum.w / n)) << 16);
+        *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+    }
+}
+
+// ---- Generic window attention, any head_dim: one wave per (window-row, head) ----
+// Lanes stride over features; online softmax over keys with wave reductions.
+__global__ void attention_generic_kernel(const void* packed_in, long long in_row, int in_elemsize, float* out,
+                                         long long out_row, const int* cu_seqlens, int window_count, int heads,
+                                         int head_dim, int sequence_tokens, float scale)
+{
+    const int wave_global = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    const int row = wave_global / heads;
+    const int head = wave_global - row * heads;
+    if (row >= sequence_tokens)
+        return;
+    int lo = 0, hi = window_count;
+    while (hi - lo > 1)
+    {
+        const int mid = (lo + hi) >> 1;
+        if (cu_seqlens[mid] <= row)
+            lo = mid;
+        else
+            hi = mid;
+    }
+    const int start = cu_seqlens[lo];
+    const int end = cu_seqlens[lo + 1];
+    constexpr int kMaxPerLane = 16; // head_dim <= 1024
+    float q[kMaxPerLane], acc[kMaxPerLane];
+    for (int j = 0; j < kMaxPerLane; j++)
+    {
+        const int f = lane + 64 * j;
+        q[j] = f < head_dim ? load_elem(packed_in, row * in_row + head * head_dim + f, in_elemsize) : 0.f;
+        acc[j] = 0.f;
+    }
+    float m = -INFINITY, l = 0.f;
+    for (int key = start; key < end; key++)
+    {
+        float dot = 0.f;
+        for (int j = 0; j < kMaxPerLane; j++)
+        {
+            const int f = lane + 64 * j;
+            if (f < head_dim)
+                dot += q[j] * load_elem(packed_in, key * in_row + (heads + head) * head_dim + f, in_elemsize);
+        }
+        for (int off = 32; off > 0; off >>= 1)
+            dot += __shfl_xor(dot, off);
+        const float s = dot * scale;
+        const float m_new = fmaxf(m, s);
+        const float alpha = __expf(m - m_new);
+        const float pk = __expf(s - m_new);
+        l = l * alpha + pk;
+        for (int j = 0; j < kMaxPerLane; j++)
+        {
+            const int f = lane + 64 * j;
+            const float v =
+                f < head_dim ? load_elem(packed_in, key * in_row + (2 * heads + head) * head_dim + f, in_elemsize) : 0.f;
+            acc[j] = acc[j] * alpha + pk * v;
+        }
+        m = m_new;
+    }
+    for (int j = 0; j < kMaxPerLane; j++)
+    {
+        const int f = lane + 64 * j;
+        if (f < head_dim)
+            out[row * out_row + head * head_dim + f] = acc[j] / l;
+    }
+}
+
+// ---- Strided cast (src/awa/shader/cast_bf16_f32.comp / cast_f32_bf16.comp semantics) ----
+__global__ void cast_kernel(const void* in, int in_elemsize, void* out, int out_elemsize, CastShape s)
+{
+    const long long total = static_cast<long long>(s.w) * s.h * s.d * s.c * s.n;
+    const long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= total)
+        return;
+    const long long plane = static_cast<long long>(s.w) * s.h * s.d;
+    const long long channel_index = idx / plane;
+    const long long inner = idx - channel_index * plane;
+    const long long b = channel_index / s.c;
+    const long long c = channel_index - b * s.c;
+    const float v = load_elem(in, b * s.in_nstep + c * s.in_cstep + inner, in_elemsize);
+    store_elem(out, b * s.out_nstep + c * s.out_cstep + inner, out_elemsize, v);
+}
+
+// ---- Seeded N(0,1): splitmix64 counter hash -> two 32-bit uniforms -> Box-Muller ----
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x)
+{
+    x += 0x9e3779b97f4a7c15ull;
+    x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ull;
+    x = (x ^ (x >> 27)) * 0x94d049bb133111ebull;
+    return x ^ (x >> 31);
+}
+
+__global__ void fill_normal_kernel(void* dst, size_t count, int elemsize, unsigned long long seed)
+{
+    const size_t pair = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const size_t i0 = 2 * pair;
+    if (i0 >= count)
+        return;
+    const uint64_t r = splitmix64(seed * 0x100000001b3ull + pair);
+    const float u1 = (static_cast<float>(static_cast<uint32_t>(r >> 32)) + 0.5f) * 2.3283064365386963e-10f;
+    const float u2 = (static_cast<float>(static_cast<uint32_t>(r)) + 0.5f) * 2.3283064365386963e-10f;
+    const float radius = sqrtf(-2.f * logf(u1));
+    float sn, cs;
+    sincosf(6.283185307179586f * u2, &sn, &cs);
+    store_elem(dst, static_cast<long long>(i0), elemsize, radius * cs);
+    if (i0 + 1 < count)
+        store_elem(dst, static_cast<long long>(i0 + 1), elemsize, radius * sn);
+}
+
+__global__ void zero_kernel(uint32_t* dst, size_t words, unsigned char* tail, size_t tail_bytes)
+{
+    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < words)
+        dst[i] = 0u;
+    if (i < tail_bytes)
+        tail[i] = 0;
+}
+
+unsigned grid_for(long long total)
+{
+    return static_cast<unsigned>((total + kBlock - 1) / kBlock);
+}
+
+} // namespace
+
+hipError_t launch_text_mean(const float* partials, int window_count, int text_tokens, int heads, int head_dim,
+                            void* text_out, long long text_token_stride, int out_elemsize, hipStream_t stream)
+{
+    const int row_elems = heads * head_dim;
+    const long long total = static_cast<long long>(text_tokens) * (row_elems / 4);
+    hipLaunchKernelGGL(text_mean_kernel, dim3(grid_for(total)), dim3(kBlock), 0, stream, partials, window_count,
+                       text_tokens, row_elems, text_out, text_token_stride, out_elemsize);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_generic(const void* packed_in, long long in_row, int in_elemsize, float* out,
+                                    long long out_row, const int* cu_seqlens_dev, int window_count, int heads,
+                                    int head_dim, int sequence_tokens, hipStream_t stream)
+{
+    if (head_dim > 1024)
+        return hipErrorInvalidValue;
+    const long long waves = static_cast<long long>(sequence_tokens) * heads;
+    const float scale = 1.f / sqrtf(static_cast<float>(head_dim));
+    hipLaunchKernelGGL(attention_generic_kernel, dim3(grid_for(waves * 64)), dim3(kBlock), 0, stream, packed_in,
+                       in_row, in_elemsize, out, out_row, cu_seqlens_dev, window_count, heads, head_dim,
+                       sequence_tokens, scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack(const RowInfo* rows, int sequence_tokens, int source_tokens, const QkvSource& video,
+                       const QkvSource& text, int heads, int head_dim, float* packed, long long packed_row,
+                       hipStream_t stream)
+{
+    const long long total = static_cast<long long>(sequence_tokens) * 3 * heads * head_dim;
+    hipLaunchKernelGGL(pack_kernel, dim3(grid_for(total)), dim3(kBlock), 0, stream, rows, sequence_tokens,
+                       source_tokens, video, text, heads, head_dim, packed, packed_row);
+    return hipGetLastError();
+}
+
+hipError_t launch_cu_seqlens(const int* cu_dev, int count, float* out, hipStream_t stream)
+{
+    hipLaunchKernelGGL(cu_seqlens_kernel, dim3(grid_for(count)), dim3(kBlock), 0, stream, cu_dev, count, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_mmrope(const RowInfo* rows, int sequence_tokens, const void* in, long long in_row,
+                         int in_elemsize, float* out, long long out_row, int heads, int head_dim, int rope_dim,
+                         int rope_pairs, const float* rope_cs, hipStream_t stream)
+{
+    const long long total = static_cast<long long>(sequence_tokens) * (3 * heads * head_dim / 2);
+    hipLaunchKernelGGL(mmrope_kernel, dim3(grid_for(total)), dim3(kBlock), 0, stream, rows, sequence_tokens, in,
+                       in_row, in_elemsize, out, out_row, heads, head_dim, rope_dim, rope_pairs, rope_cs);
+    return hipGetLastError();
+}
+
+hipError_t launch_unpack_video(const int* video_positions, int source_t, int source_h, int source_w,
+                               const void* packed, long long packed_row, int packed_elemsize, const VideoSink& out,
+                               int heads, int head_dim, hipStream_t stream)
+{
+    const int row_elems = heads * head_dim;
+    const long long total = static_cast<long long>(source_t) * source_h * source_w * row_elems;
+    hipLaunchKernelGGL(unpack_video_kernel, dim3(grid_for(total)), dim3(kBlock), 0, stream, video_positions,
+                       source_t, source_h, source_w, packed, packed_row, packed_elemsize, out, row_elems);
+    return hipGetLastError();
+}
+
+hipError_t launch_unpack_text(const int* text_positions, int window_count, int text_tokens, const void* packed,
+                              long long packed_row, int packed_elemsize, void* out, long long out_row,
+                              int out_elemsize, int heads, int head_dim, hipStream_t stream)
+{
+    const int row_elems = heads * head_dim;
+    const long long total = static_cast<long long>(text_tokens) * row_elems;
+    hipLaunchKernelGGL(unpack_text_kernel, dim3(grid_for(total)), dim3(kBlock), 0, stream, text_positions,
+                       window_count, text_tokens, packed, packed_row, packed_elemsize, out, out_row, out_elemsize,
+                       row_elems);
+    return hipGetLastError();
+}
+
+hipError_t launch_cast(const void* in, int in_elemsize, void* out, int out_elemsize, const CastShape& s,
+                       hipStream_t stream)
+{
+    const long long total = static_cast<long long>(s.w) * s.h * s.d * s.c * s.n;
+    hipLaunchKernelGGL(cast_kernel, dim3(grid_for(total)), dim3(kBlock), 0, stream, in, in_elemsize, out,
+                       out_elemsize, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_normal(void* dst, size_t count, int elemsize, unsigned long long seed, hipStream_t stream)
+{
+    const long long pairs = static_cast<long long>((count + 1) / 2);
+    hipLaunchKernelGGL(fill_normal_kernel, dim3(grid_for(pairs)), dim3(kBlock), 0, stream, dst, count, elemsize,
+                       seed);
+    return hipGetLastError();
+}
+
+hipError_t launch_zero(void* dst, size_t bytes, hipStream_t stream)
+{
+    const size_t words = bytes / 4;
+    const size_t tail = bytes - words * 4;
+    const long long threads = static_cast<long long>(words > tail ? words : tail);
+    if (threads == 0)
+        return hipSuccess;
+    hipLaunchKernelGGL(zero_kernel, dim3(grid_for(threads)), dim3(kBlock), 0, stream, static_cast<uint32_t*>(dst),
+                       words, static_cast<unsigned char*>(dst) + words * 4, tail);
+    return hipGetLastError();
+}
+
+} // namespace awa

@@ -1,0 +1,118 @@
+"""Parity of the fused HIP layer (awa_forward) with the CPU oracle.
+
+Tolerances: fp32 compute, max abs error <= 1e-4 against the oracle's Kahan
+(shader-order) fp32 result; bf16 compute, max|err| / max|ref| <= 2e-2 against
+the same oracle fed the identical bf16-rounded inputs.
+"""
+
+import numpy as np
+import pytest
+
+import awa_hip as A
+import oracle as O
+from awa_cases import CONFIGS, HEAD_DIM, RAGGED, abs_err, geometry, qkv_inputs, rel_err
+from device_blobs import qkv_blob, read_mat3, read_video, video_out_blob, mat3
+
+pytestmark = pytest.mark.gpu
+
+FP32_ATOL = 1e-4
+BF16_RTOL = 2e-2
+
+
+def run_fused(g, video, text, compute, in_elem=4, out_elem=4, layout="a", batch_out=False):
+    heads = video.shape[2]
+    plan = A.Plan(A.LayerParams(*g.args, g.text_tokens, g.shifted))
+    plan.upload()
+    vq = qkv_blob(video, layout, in_elem)
+    tq = qkv_blob(text, "a", in_elem)
+    vo = video_out_blob(g.t, g.h, g.w, heads, HEAD_DIM, out_elem, batch_out)
+    to = mat3(HEAD_DIM, heads, g.text_tokens, out_elem)
+    plan.forward(vq.blob, tq.blob, vo.blob, to.blob, compute)
+    A.synchronize()
+    return read_video(vo, g.t, g.h, g.w, heads, HEAD_DIM), read_mat3(to)
+
+
+def bf16_round(x):
+    return A.bf16_bits_to_f32(A.f32_to_bf16_bits(x))
+
+
+@pytest.mark.parametrize("shifted", [False, True])
+def test_fp32_image_layer(gpu, shifted):
+    g = geometry(CONFIGS["image_1x16x16"], shifted)
+    print(f"case fp32 image shifted={shifted}", flush=True)
+    video, text = qkv_inputs(g, 20, HEAD_DIM, 20260823)
+    ref_v, ref_t = O.awa_layer(g, video, text, 20, HEAD_DIM)
+    got_v, got_t = run_fused(g, video, text, A.COMPUTE_F32)
+    assert abs_err(got_v, ref_v) <= FP32_ATOL
+    assert abs_err(got_t, ref_t) <= FP32_ATOL
+
+
+@pytest.mark.parametrize("shifted", [False, True])
+def test_bf16_clip_layer(gpu, shifted):
+    g = geometry(CONFIGS["clip_2x16x16"], shifted)
+    print(f"case bf16 clip_2x16x16 shifted={shifted}", flush=True)
+    video, text = qkv_inputs(g, 20, HEAD_DIM, 20260824)
+    video, text = bf16_round(video), bf16_round(text)
+    ref_v, ref_t = O.awa_layer(g, video, text, 20, HEAD_DIM)
+    got_v, got_t = run_fused(g, video, text, A.COMPUTE_BF16, in_elem=2, out_elem=2)
+    assert rel_err(got_v, ref_v) <= BF16_RTOL
+    assert rel_err(got_t, ref_t) <= BF16_RTOL
+
+
+@pytest.mark.parametrize("params", RAGGED)
+@pytest.mark.parametrize("shifted", [False, True])
+def test_fp32_ragged(gpu, params, shifted):
+    g = geometry(params, shifted)
+    print(f"case fp32 ragged {params} shifted={shifted}", flush=True)
+    video, text = qkv_inputs(g, 2, HEAD_DIM, 7 + sum(params))
+    ref_v, ref_t = O.awa_layer(g, video, text, 2, HEAD_DIM)
+    got_v, got_t = run_fused(g, video, text, A.COMPUTE_F32)
+    assert abs_err(got_v, ref_v) <= FP32_ATOL
+    assert abs_err(got_t, ref_t) <= FP32_ATOL
+
+
+@pytest.mark.parametrize("params", RAGGED[:2])
+def test_bf16_ragged(gpu, params):
+    g = geometry(params, True)
+    print(f"case bf16 ragged {params}", flush=True)
+    video, text = qkv_inputs(g, 3, HEAD_DIM, 11 + sum(params))
+    video, text = bf16_round(video), bf16_round(text)
+    ref_v, ref_t = O.awa_layer(g, video, text, 3, HEAD_DIM)
+    got_v, got_t = run_fused(g, video, text, A.COMPUTE_BF16, in_elem=2, out_elem=4)
+    assert rel_err(got_v, ref_v) <= BF16_RTOL
+    assert rel_err(got_t, ref_t) <= BF16_RTOL
+
+
+def test_production_single_window(gpu):
+    """(4,3,3) at 256x256 is a single 1x16x16 window: plain attention over N+T_x tokens."""
+    g = geometry(CONFIGS["production_256"], False)
+    print("case production single window", flush=True)
+    video, text = qkv_inputs(g, 4, HEAD_DIM, 666)
+    ref_v, ref_t = O.awa_layer(g, video, text, 4, HEAD_DIM)
+    got_v, got_t = run_fused(g, video, text, A.COMPUTE_F32)
+    assert abs_err(got_v, ref_v) <= FP32_ATOL
+    assert abs_err(got_t, ref_t) <= FP32_ATOL
+
+
+@pytest.mark.parametrize("layout", ["a", "b", "c", "d"])
+@pytest.mark.parametrize("batch_out", [False, True])
+def test_layouts_identical(gpu, layout, batch_out):
+    """All four accepted QKV layouts and both video output layouts give the same bits."""
+    g = geometry((2, 8, 12, 1, 4, 4, 6), True)
+    print(f"case layout {layout} batch_out={batch_out}", flush=True)
+    video, text = qkv_inputs(g, 3, HEAD_DIM, 99)
+    base_v, base_t = run_fused(g, video, text, A.COMPUTE_F32, layout="a", batch_out=False)
+    got_v, got_t = run_fused(g, video, text, A.COMPUTE_F32, layout=layout, batch_out=batch_out)
+    np.testing.assert_array_equal(got_v, base_v)
+    np.testing.assert_array_equal(got_t, base_t)
+
+
+def test_bf16_output_rounding(gpu):
+    """bf16 outputs are the fp32 outputs rounded to nearest even."""
+    g = geometry((1, 8, 8, 1, 2, 2, 4), True)
+    print("case bf16 output rounding", flush=True)
+    video, text = qkv_inputs(g, 2, HEAD_DIM, 5)
+    v32, t32 = run_fused(g, video, text, A.COMPUTE_F32, out_elem=4)
+    v16, t16 = run_fused(g, video, text, A.COMPUTE_F32, out_elem=2)
+    np.testing.assert_array_equal(v16, bf16_round(v32))
+    np.testing.assert_array_equal(t16, bf16_round(t32))
