@@ -1,0 +1,221 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X AWA path on the 33-frame 256x256 DiT attention stack.
+
+Workload: the AWA layer of all 32 DiT blocks at latent 9x16x16 (N = 2304
+video tokens), window counts (3, 8, 8) -> 3x8x8 windows, 64 text tokens,
+20 heads x 128. Blocks 0-8 compute in fp32, blocks 9-31 in bf16; even blocks
+use unshifted windows (12 windows of 256 tokens), odd blocks shifted ones
+(36 ragged windows of 80..256 tokens). Every block reads its own QKV (fp32 or
+bf16, synthetic N(0,1) generated on the device and resident in HBM before
+timing) and writes its own outputs. One step = the 32 layers on one stream,
+including the fp32 -> bf16 conversion at block 9.
+
+Prints one JSON line: the step's window-attention throughput (TFLOP/s over
+the algorithmic FLOPs sum_w 4 L_w^2 d H), ms per step, the bf16 layers' share
+of bf16 MFMA peak, the roofline entry of the dominant kernel (the fp32
+attention kernel, timed with HIP events on its own stream) and the CPU
+baseline (the oracle's single-threaded restatement of the reference's CPU
+layer, on a bounded sample).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "seedvr2-ncnn_amd"))
+
+METRIC = "window-attn TFLOP/s & % bf16 MFMA peak; ms per 32-block DiT step, 33f 256²"
+GRID = (9, 16, 16)
+WINDOWS = (3, 8, 8)
+TEXT = 64
+HEADS = 20
+HEAD_DIM = 128
+BLOCKS = 32
+FP32_PREFIX = 9
+PEAK_BF16 = 2.5e15
+PEAK_FP32 = 157.3e12
+PEAK_HBM = 8.0e12
+
+
+def cpu_baseline(sample_layers: int) -> dict:
+    """Single-threaded CPU restatement of the reference's CPU AWA forward
+    (Pack -> MMRoPE -> WindowAttention -> Unpack in the reference's loop order)
+    on one unshifted and one shifted layer of this workload, projected to the
+    32-block step (16 layers of each)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    O.set_num_threads(1)
+    times = []
+    flops = []
+    for shifted in (False, True)[:sample_layers]:
+        g = O.Geometry(*GRID, *WINDOWS, TEXT, shifted)
+        n = g.source_tokens * 3 * HEADS * HEAD_DIM
+        video = O.fill_gaussian(n, 20260825, 0).reshape(g.source_tokens, 3, HEADS, HEAD_DIM)
+        text = O.fill_gaussian(TEXT * 3 * HEADS * HEAD_DIM, 20260825, 1).reshape(TEXT, 3, HEADS, HEAD_DIM)
+        cu = O.build_maps(g).cu_seqlens
+        flops.append(float(sum(4.0 * (b - a) ** 2 * HEAD_DIM * HEADS for a, b in zip(cu[:-1], cu[1:]))))
+        t0 = time.perf_counter()
+        O.awa_layer(g, video, text, HEADS, HEAD_DIM, attention_order="cpu", text_order="cpu")
+        times.append(time.perf_counter() - t0)
+    step_s = 16.0 * sum(times) * (2 / len(times))
+    step_flops = 16.0 * sum(flops) * (2 / len(flops))
+    return {
+        "value": step_flops / step_s / 1e12,
+        "unit": "TFLOP/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"one unshifted and one shifted fp32 layer of this workload ({', '.join(f'{t:.2f}' for t in times)} s), "
+                   f"single thread, reference CPU loop order; projected 32-block step {step_s * 1e3:.0f} ms"),
+        "ms_per_step": step_s * 1e3,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--profile-steps", type=int, default=5, help="steps with per-block event timing")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-layers", type=int, default=2, choices=(1, 2))
+    ap.add_argument("--traffic-json", default=None,
+                    help="JSON with measured HBM bytes per launch of the dominant kernel (from rocprofv3 --pmc)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import awa_hip as A
+
+    A.init(0)
+    t, h, w = GRID
+    N = t * h * w
+    row_qkv = 3 * HEADS * HEAD_DIM
+    row_out = HEADS * HEAD_DIM
+    buffers = []
+    vq, tq, vo, to = [], [], [], []
+    for b in range(BLOCKS):
+        es = 4 if b < FP32_PREFIX else 2
+        bufs = [A.DeviceBuffer(N * row_qkv * es), A.DeviceBuffer(TEXT * row_qkv * es),
+                A.DeviceBuffer(N * row_out * es), A.DeviceBuffer(TEXT * row_out * es)]
+        bufs[0].fill_normal(N * row_qkv, es, 20260825 * 64 + 2 * b)
+        bufs[1].fill_normal(TEXT * row_qkv, es, 20260825 * 64 + 2 * b + 1)
+        buffers.append(bufs)
+        vq.append(bufs[0].ptr)
+        tq.append(bufs[1].ptr)
+        vo.append(bufs[2].ptr)
+        to.append(bufs[3].ptr)
+    stream = A.Stream()
+    stack = A.AttentionStack(*GRID, *WINDOWS, TEXT, BLOCKS, FP32_PREFIX, HEADS, HEAD_DIM)
+    A.synchronize()
+
+    for _ in range(args.warmup):
+        stack.run(vq, tq, vo, to, stream)
+    stream.synchronize()
+    start, stop = A.Event(), A.Event()
+    wall0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(args.steps):
+        stack.run(vq, tq, vo, to, stream)
+    stop.record(stream)
+    stream.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_per_step = start.elapsed_ms(stop) / args.steps
+
+    # Per-block kernel times (HIP events on the stack's stream around each attention kernel).
+    stack.set_profiling(True)
+    att = np.zeros(BLOCKS)
+    blk = np.zeros(BLOCKS)
+    for _ in range(args.profile_steps):
+        stack.run(vq, tq, vo, to, stream)
+        stream.synchronize()
+        a, b_ = stack.block_times()
+        att += a
+        blk += b_
+    att /= args.profile_steps
+    blk /= args.profile_steps
+    flops = stack.block_flops()
+    step_flops = float(flops.sum())
+
+    fp32_idx = np.arange(FP32_PREFIX)
+    bf16_idx = np.arange(FP32_PREFIX, BLOCKS)
+    # Dominant kernel by total time per step.
+    fp32_total, bf16_total = att[fp32_idx].sum(), att[bf16_idx].sum()
+    dom = fp32_idx if fp32_total >= bf16_total else bf16_idx
+    dom_name = "window_attention_kernel<f32 MFMA>" if fp32_total >= bf16_total else "window_attention_kernel<bf16 MFMA>"
+    avg_flops = float(flops[dom].mean())
+    avg_ms = float(att[dom].mean())
+    achieved = avg_flops / (avg_ms * 1e-3) / 1e12
+    peak = (PEAK_FP32 if fp32_total >= bf16_total else PEAK_BF16) / 1e12
+    traffic = None
+    if args.traffic_json and os.path.exists(args.traffic_json):
+        with open(args.traffic_json) as f:
+            traffic = json.load(f).get("bytes_per_launch")
+
+    def layer_stats(idx):
+        ms = float(att[idx].mean())
+        fl = float(flops[idx].mean())
+        return {"kernel_ms": round(ms, 5), "layer_ms": round(float(blk[idx].mean()), 5),
+                "tflops": round(fl / (ms * 1e-3) / 1e12, 2),
+                "pct_bf16_peak": round(100.0 * fl / (ms * 1e-3) / PEAK_BF16, 2)}
+
+    even = lambda idx: idx[idx % 2 == 0]
+    odd = lambda idx: idx[idx % 2 == 1]
+    bf16_layers = {"unshifted": layer_stats(even(bf16_idx)), "shifted": layer_stats(odd(bf16_idx))}
+    fp32_layers = {"unshifted": layer_stats(even(fp32_idx)), "shifted": layer_stats(odd(fp32_idx))}
+    bf16_all_ms = float(att[bf16_idx].sum())
+    bf16_pct = 100.0 * float(flops[bf16_idx].sum()) / (bf16_all_ms * 1e-3) / PEAK_BF16
+
+    result = {
+        "metric": METRIC,
+        "value": round(step_flops / (ms_per_step * 1e-3) / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32+bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "dit32_awa_attention_33f_256 (latent 9x16x16, windows 3x8x8, 64 text, 20x128 heads)",
+            "latent": list(GRID), "window_counts": list(WINDOWS), "text_tokens": TEXT, "heads": HEADS,
+            "head_dim": HEAD_DIM, "blocks": BLOCKS, "fp32_prefix_blocks": FP32_PREFIX,
+            "step_gflop": round(step_flops / 1e9, 3), "wall_ms_per_step": round(wall * 1e3 / args.steps, 4),
+        },
+        "bf16_layers": {**bf16_layers, "pct_bf16_peak_all": round(bf16_pct, 2)},
+        "fp32_layers": {k: {**v, "pct_fp32_peak": round(v["tflops"] * 1e12 / PEAK_FP32 * 100, 2)}
+                        for k, v in fp32_layers.items()},
+        "roofline": {
+            "kernel": dom_name,
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": round(peak, 1),
+            "unit": "TFLOP/s",
+            "frac": round(achieved / peak, 4),
+            "traffic": traffic,
+            "flops_per_launch": avg_flops,
+            "avg_launch_ms": round(avg_ms, 5),
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(args.cpu_sample_layers)
+    print(json.dumps(result), flush=True)
+    stack.destroy()
+    stream.destroy()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

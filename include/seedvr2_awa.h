@@ -164,6 +164,42 @@ int awa_unpack(const awa_plan* plan, const awa_blob* packed, const awa_blob* vid
  * the block-9 precision switch convert_precision_gpu, src/dit/dit_stack.cpp:329-357). */
 int awa_cast(const awa_blob* input, const awa_blob* output, void* stream);
 
+/* ---- DiT attention stack: the AWA layer of every block with the precision dispatch ---- */
+
+/* Mirrors DitStackSession's block loop (src/dit/dit_stack.cpp:497-565, :931-982):
+ * blocks [0, fp32_prefix_blocks) compute in fp32 (fp32 QKV in and out), the
+ * rest in bf16; even blocks use unshifted windows, odd blocks shifted
+ * (tools/reference/dit_stack.py:75-79); one stream. */
+typedef struct awa_stack_desc {
+    int source_t, source_h, source_w;    /* session token grid (AwaRuntimeSpec) */
+    int windows_t, windows_h, windows_w; /* window counts (params 3/4/5) */
+    int text_tokens;
+    int blocks;             /* 32 */
+    int fp32_prefix_blocks; /* 9 (src/dit/dit_stack.cpp:519) */
+    int heads, head_dim;    /* 20, 128 */
+} awa_stack_desc;
+
+typedef struct awa_stack awa_stack;
+
+int awa_stack_create(const awa_stack_desc* desc, awa_stack** stack);
+void awa_stack_destroy(awa_stack* stack);
+/* Per-block device pointers, dense token-major: video_qkv[b] [N][3][H][d],
+ * text_qkv[b] [T_x][3][H][d], video_out[b] [N][H][d], text_out[b] [T_x][H][d];
+ * fp32 for blocks below fp32_prefix_blocks, bf16 from there on. At the first
+ * bf16 block the previous block's outputs are converted to bf16 into the
+ * stack's carry buffers, as convert_precision_gpu does at block 9
+ * (src/dit/dit_stack.cpp:934-950). */
+int awa_stack_run(awa_stack* stack, void* const* video_qkv, void* const* text_qkv, void* const* video_out,
+                  void* const* text_out, void* stream);
+/* Optional per-block timing (the reference's --profile surface): when enabled
+ * each run records events around every block's attention kernel. */
+int awa_stack_set_profiling(awa_stack* stack, int enabled);
+/* After a profiled run has completed: milliseconds of each block's attention
+ * kernel and of the block's layer (attention kernel + text mean). */
+int awa_stack_block_times(const awa_stack* stack, float* attention_ms, float* block_ms);
+/* Algorithmic FLOPs of each block: sum over windows of 4 * L^2 * head_dim * heads. */
+int awa_stack_block_flops(const awa_stack* stack, double* flops);
+
 #ifdef __cplusplus
 }
 #endif

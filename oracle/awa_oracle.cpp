@@ -22,6 +22,10 @@
 #include <random>
 #include <vector>
 
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
 namespace
 {
 
@@ -139,6 +143,18 @@ float kahan_add(float sum, float term_in, float& correction)
 } // namespace
 
 extern "C" {
+
+// Thread count of the (window, head)-parallel loops; 1 reproduces the
+// reference's single-threaded CPU layers.
+int orc_set_num_threads(int threads)
+{
+    if (threads < 1)
+        return -1;
+#ifdef _OPENMP
+    omp_set_num_threads(threads);
+#endif
+    return 0;
+}
 
 int orc_python_round_positive(double value)
 {

@@ -30,6 +30,7 @@ def lib() -> ctypes.CDLL:
         if not os.path.exists(path):
             raise RuntimeError(f"oracle library missing: {path} (run `make -C oracle`)")
         _LIB = ctypes.CDLL(path)
+        _LIB.orc_set_num_threads.argtypes = [_i]
         _LIB.orc_python_round_positive.argtypes = [ctypes.c_double]
         _LIB.orc_make_windows.argtypes = [_i] * 7 + [_p, _i]
         _LIB.orc_map_sizes.argtypes = [_i] * 8 + [_p]
@@ -84,6 +85,12 @@ class Geometry:
     @property
     def source_tokens(self) -> int:
         return self.t * self.h * self.w
+
+
+def set_num_threads(threads: int) -> None:
+    """Threads of the oracle's (window, head) loops; 1 = the reference's single thread."""
+    if lib().orc_set_num_threads(int(threads)) != 0:
+        raise ValueError("threads must be >= 1")
 
 
 def python_round_positive(x: float) -> int:

@@ -35,6 +35,8 @@ EXPORTED_SYMBOLS = (
     "awa_plan_info_get", "awa_plan_windows", "awa_plan_sequence_index", "awa_plan_cu_seqlens",
     "awa_plan_video_positions", "awa_plan_text_positions", "awa_plan_rope_table", "awa_plan_upload",
     "awa_forward", "awa_pack", "awa_mmrope", "awa_window_attention", "awa_unpack", "awa_cast",
+    "awa_stack_create", "awa_stack_destroy", "awa_stack_run", "awa_stack_set_profiling", "awa_stack_block_times",
+    "awa_stack_block_flops",
 )
 
 
@@ -57,6 +59,12 @@ class AwaPlanDesc(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int) for name in (
         "source_t", "source_h", "source_w", "windows_t", "windows_h", "windows_w", "text_tokens", "shifted",
         "rope_dim", "runtime_t", "runtime_h", "runtime_w", "runtime_tokens")]
+
+
+class AwaStackDesc(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_int) for name in (
+        "source_t", "source_h", "source_w", "windows_t", "windows_h", "windows_w", "text_tokens", "blocks",
+        "fp32_prefix_blocks", "heads", "head_dim")]
 
 
 class AwaPlanInfo(ctypes.Structure):
@@ -110,6 +118,14 @@ def lib() -> ctypes.CDLL:
         L.awa_window_attention.argtypes = [vp, bp, bp, i, vp]
         L.awa_unpack.argtypes = [vp, bp, bp, bp, vp]
         L.awa_cast.argtypes = [bp, bp, vp]
+        L.awa_stack_create.argtypes = [ctypes.POINTER(AwaStackDesc), ctypes.POINTER(vp)]
+        L.awa_stack_destroy.argtypes = [vp]
+        L.awa_stack_destroy.restype = None
+        vpp = ctypes.POINTER(vp)
+        L.awa_stack_run.argtypes = [vp, vpp, vpp, vpp, vpp, vp]
+        L.awa_stack_set_profiling.argtypes = [vp, i]
+        L.awa_stack_block_times.argtypes = [vp, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float)]
+        L.awa_stack_block_flops.argtypes = [vp, ctypes.POINTER(ctypes.c_double)]
         _LIB = L
     return _LIB
 
@@ -338,6 +354,49 @@ class Plan:
     def unpack(self, packed: AwaBlob, video_out: AwaBlob, text_out: AwaBlob, stream: Optional[Stream] = None) -> None:
         check(lib().awa_unpack(self.h, ctypes.byref(packed), ctypes.byref(video_out), ctypes.byref(text_out),
                                _s(stream)), "awa_unpack")
+
+
+class AttentionStack:
+    """The DiT attention stack (awa_stack_*): per-block AWA with the fp32/bf16 dispatch."""
+
+    def __init__(self, t: int, h: int, w: int, nt: int, nh: int, nw: int, text_tokens: int, blocks: int = 32,
+                 fp32_prefix_blocks: int = 9, heads: int = 20, head_dim: int = 128):
+        self.desc = AwaStackDesc(t, h, w, nt, nh, nw, text_tokens, blocks, fp32_prefix_blocks, heads, head_dim)
+        p = ctypes.c_void_p()
+        check(lib().awa_stack_create(ctypes.byref(self.desc), ctypes.byref(p)), "awa_stack_create")
+        self.handle = p.value
+        self.blocks = blocks
+
+    def run(self, video_qkv: Sequence[int], text_qkv: Sequence[int], video_out: Sequence[int],
+            text_out: Sequence[int], stream: Optional[Stream] = None) -> None:
+        arr = ctypes.c_void_p * self.blocks
+        check(lib().awa_stack_run(ctypes.c_void_p(self.handle), arr(*video_qkv), arr(*text_qkv), arr(*video_out),
+                                  arr(*text_out), _s(stream)), "awa_stack_run")
+
+    def set_profiling(self, enabled: bool) -> None:
+        check(lib().awa_stack_set_profiling(ctypes.c_void_p(self.handle), int(enabled)), "awa_stack_set_profiling")
+
+    def block_times(self):
+        att = (ctypes.c_float * self.blocks)()
+        blk = (ctypes.c_float * self.blocks)()
+        check(lib().awa_stack_block_times(ctypes.c_void_p(self.handle), att, blk), "awa_stack_block_times")
+        return np.array(att[:], np.float64), np.array(blk[:], np.float64)
+
+    def block_flops(self) -> np.ndarray:
+        f = (ctypes.c_double * self.blocks)()
+        check(lib().awa_stack_block_flops(ctypes.c_void_p(self.handle), f), "awa_stack_block_flops")
+        return np.array(f[:], np.float64)
+
+    def destroy(self) -> None:
+        if self.handle:
+            lib().awa_stack_destroy(ctypes.c_void_p(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
 
 
 def cast(inp: AwaBlob, out: AwaBlob, stream: Optional[Stream] = None) -> None:

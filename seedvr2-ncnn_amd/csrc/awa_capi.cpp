@@ -11,6 +11,7 @@
 #include <string>
 #include <vector>
 
+#include "awa_internal.h"
 #include "awa_kernels.h"
 #include "awa_plan.h"
 #include "seedvr2_awa.h"
@@ -569,6 +570,23 @@ int awa_plan_upload(awa_plan* plan, void* stream)
 int awa_forward(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv, const awa_blob* video_out,
                 const awa_blob* text_out, int compute, void* stream)
 {
+    return awa::forward_fused(plan, video_qkv, text_qkv, video_out, text_out, compute, as_stream(stream), nullptr);
+}
+
+} // extern "C"
+
+namespace awa
+{
+
+void set_error(const std::string& message)
+{
+    g_last_error = message;
+}
+
+int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv,
+                  const awa_blob* video_out, const awa_blob* text_out, int compute, hipStream_t stream,
+                  hipEvent_t after_attention)
+{
     int rc = check_plan_uploaded(plan);
     if (rc != AWA_OK)
         return rc;
@@ -621,13 +639,18 @@ int awa_forward(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob*
     p.source_h = plan->source_h;
     p.source_w = plan->source_w;
     p.scale_log2 = (1.f / std::sqrt(static_cast<float>(vl.head_dim))) * 1.4426950408889634f;
-    hipStream_t s = as_stream(stream);
-    HIP_TRY(awa::launch_attention(p, s), "attention kernel launch");
+    HIP_TRY(awa::launch_attention(p, stream), "attention kernel launch");
+    if (after_attention)
+        HIP_TRY(hipEventRecord(after_attention, stream), "hipEventRecord");
     HIP_TRY(awa::launch_text_mean(plan->text_partials, static_cast<int>(plan->windows.size()), plan->text_tokens,
-                                  vl.heads, vl.head_dim, text_out->data, text_out->cstep, text_out->elemsize, s),
+                                  vl.heads, vl.head_dim, text_out->data, text_out->cstep, text_out->elemsize, stream),
             "text mean kernel launch");
     return AWA_OK;
 }
+
+} // namespace awa
+
+extern "C" {
 
 int awa_pack(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv, const awa_blob* packed,
              const awa_blob* cu_seqlens, void* stream)
