@@ -6,11 +6,13 @@
 // statistics of a query live in two lanes (lane and lane^32), and the
 // rescale of the output accumulator O^T = V^T P^T is lane-local.
 //
-// K and V tiles of 32 keys are staged through LDS (K row-major, V transposed
-// so that the PV operand reads are contiguous in the key index). Keys are
-// read out of the K tile in an order (bits 2 and 3 of the row swapped) that
-// makes every lane's 16 probabilities cover two runs of 8 consecutive keys,
-// which is exactly the K-slot layout of the B operand of the PV MFMA.
+// K and V tiles (64 keys for bf16, 32 for fp32) are staged through LDS (K
+// row-major, V transposed so that the PV operand reads are contiguous in the
+// key index). Keys are read out of the K tile in an order (bits 2 and 3 of the
+// row swapped) that makes every lane's 16 probabilities of a 32-key block
+// cover two runs of 8 consecutive keys, which is exactly the K-slot layout of
+// the B operand of the PV MFMA. bf16 tiles hold two 32-key blocks whose
+// score MFMA chains are interleaved.
 //
 // In fused mode the kernel gathers rows straight from the video / text QKV
 // blobs using the window geometry (the reference's Pack), applies the 3-axis
@@ -18,6 +20,13 @@
 // their grid position (Unpack); text rows go to per-window partials that a
 // second kernel averages in window order. Packed mode reads a packed
 // [S][3H][d] blob and writes [S][H][d], for the staged WindowAttention layer.
+//
+// Per-tile VALU work is kept small: the window's row -> (grid position, RoPE
+// coordinates) table is built once per workgroup in LDS, the softmax scale is
+// folded into Q, masking only runs on a ragged last tile, and the output
+// accumulator is only rescaled when a row maximum grows by more than 2^8
+// (exact: numerator and denominator share the stale maximum). The next
+// tile's global loads are in flight while the current tile is computed.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -30,98 +39,164 @@ namespace
 {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kKeyTile = 32;
+constexpr int kThreads = 64 * kQueryWaves;
 constexpr int kRopePairs = kRopeDim / 6; // 21 pairs per axis
-static_assert(kMaxRopeCoords * kRopePairs * 2 * 4 <= 24 * 1024, "RoPE table must stay small in LDS");
+constexpr int kRopeRow = 2 * kRopePairs; // floats per coordinate in the table
+constexpr float kRescaleThreshold = 8.f; // log2 units
+static_assert(kMaxRopeCoords * kRopeRow * 4 <= 24 * 1024, "RoPE table must stay small in LDS");
 
-// LDS pitches (elements). Rows stay 16-byte aligned for ds_read_b128.
-constexpr int kKPitchBf = kHeadDim + 8;   // 272 B
-constexpr int kVPitchBf = kKeyTile + 8;   // 80 B
-constexpr int kKPitchF = kHeadDim + 4;    // 528 B
-constexpr int kVPitchF = kKeyTile + 4;    // 144 B
-
-__device__ __forceinline__ float bf16_bits_to_float(uint32_t bits16)
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi)
 {
-    return __uint_as_float(bits16 << 16);
+    const bf16x2 v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+    return __builtin_bit_cast(uint32_t, v);
 }
 
-// Round to nearest even (the reference's bit formula, src/dit/shader/dit_rmsnorm.comp:47-51).
-__device__ __forceinline__ uint32_t float_to_bf16_bits(float f)
+__device__ __forceinline__ float bf16_lo(uint32_t w)
 {
-    const uint32_t bits = __float_as_uint(f);
-    return (bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16;
+    return __uint_as_float(w << 16);
 }
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi)
+__device__ __forceinline__ float bf16_hi(uint32_t w)
 {
-    return float_to_bf16_bits(lo) | (float_to_bf16_bits(hi) << 16);
+    return __uint_as_float(w & 0xffff0000u);
 }
 
-// Loads 8 consecutive elements as floats (16-byte aligned source).
-__device__ __forceinline__ void load8(const float* p, float v[8])
-{
-    const float4 a = *reinterpret_cast<const float4*>(p);
-    const float4 b = *reinterpret_cast<const float4*>(p + 4);
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-}
-
-__device__ __forceinline__ void load8(const uint16_t* p, float v[8])
+// Raw 8-element loads (16-byte aligned): bf16 -> 4 words, fp32 -> 8 words.
+__device__ __forceinline__ void load_raw8(const uint16_t* p, uint32_t* w)
 {
     const uint4 a = *reinterpret_cast<const uint4*>(p);
-    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-    for (int i = 0; i < 4; i++)
+    w[0] = a.x;
+    w[1] = a.y;
+    w[2] = a.z;
+    w[3] = a.w;
+}
+
+__device__ __forceinline__ void load_raw8(const float* p, uint32_t* w)
+{
+    const uint4 a = *reinterpret_cast<const uint4*>(p);
+    const uint4 b = *reinterpret_cast<const uint4*>(p + 4);
+    w[0] = a.x;
+    w[1] = a.y;
+    w[2] = a.z;
+    w[3] = a.w;
+    w[4] = b.x;
+    w[5] = b.y;
+    w[6] = b.z;
+    w[7] = b.w;
+}
+
+template <typename TIn>
+constexpr int kRawWords8 = sizeof(TIn) == 2 ? 4 : 8; // words per 8 elements
+
+template <typename TIn>
+__device__ __forceinline__ void raw_to_float8(const uint32_t* w, float* v)
+{
+    if constexpr (sizeof(TIn) == 2)
     {
-        v[2 * i] = bf16_bits_to_float(w[i] & 0xffffu);
-        v[2 * i + 1] = bf16_bits_to_float(w[i] >> 16);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+        {
+            v[2 * i] = bf16_lo(w[i]);
+            v[2 * i + 1] = bf16_hi(w[i]);
+        }
+    }
+    else
+    {
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            v[i] = __uint_as_float(w[i]);
     }
 }
 
-// Interleaved-pair rotation of 8 features starting at feature f0 (even):
-// even' = x_even*cos - x_odd*sin, odd' = x_odd*cos + x_even*sin, for features
-// below kRopeDim; the axis of pair p is p / 21. No contraction, so the result
-// is bit-identical to the reference's CPU rotation.
-__device__ __forceinline__ void rope8(float v[8], int f0, int ct, int ch, int cw, const float* table)
+// One interleaved RoPE pair: even' = x0*cos - x1*sin, odd' = x1*cos + x0*sin.
+// No contraction, so the result is bit-identical to the reference's CPU rotation.
+__device__ __forceinline__ void rope_pair_cs(float& x0, float& x1, float c, float s)
 {
 #pragma clang fp contract(off)
+    const float a = x0;
+    const float b = x1;
+    x0 = a * c - b * s;
+    x1 = b * c + a * s;
+}
+
+// The same rotation with fused multiply-adds, for operands that are rounded
+// to bf16 right after (the two forms differ by at most an fp32 ulp).
+__device__ __forceinline__ void rope_pair_fma(float& x0, float& x1, float c, float s)
+{
+    const float a = x0;
+    const float b = x1;
+    x0 = fmaf(a, c, -(b * s));
+    x1 = fmaf(b, c, a * s);
+}
+
+__device__ __forceinline__ void rope_pair(float& x0, float& x1, const float* cs)
+{
+    const float2 t = *reinterpret_cast<const float2*>(cs);
+    rope_pair_cs(x0, x1, t.x, t.y);
+}
+
+// Rotates kPairs consecutive feature pairs starting at pair kPair0 (both
+// compile-time, so each pair's axis and table column fold to constants) of a
+// row with RoPE coordinates (ct, ch, cw). Pair p belongs to axis p / 21;
+// pairs at or beyond rope_dim / 2 are left unchanged.
+template <int kPair0, int kPairs>
+__device__ __forceinline__ void rope_fixed(float* v, int ct, int ch, int cw, const float* table)
+{
 #pragma unroll
-    for (int q = 0; q < 4; q++)
+    for (int q = 0; q < kPairs; q++)
     {
-        const int f = f0 + 2 * q;
-        if (f < kRopeDim)
+        const int pair = kPair0 + q;
+        if (2 * pair < kRopeDim)
         {
-            const int pair = f >> 1;
             const int axis = pair / kRopePairs;
-            const int pp = pair - axis * kRopePairs;
             const int coord = axis == 0 ? ct : (axis == 1 ? ch : cw);
-            const float c = table[(coord * kRopePairs + pp) * 2];
-            const float s = table[(coord * kRopePairs + pp) * 2 + 1];
-            const float x0 = v[2 * q];
-            const float x1 = v[2 * q + 1];
-            v[2 * q] = x0 * c - x1 * s;
-            v[2 * q + 1] = x1 * c + x0 * s;
+            rope_pair(v[2 * q], v[2 * q + 1], table + coord * kRopeRow + 2 * (pair - axis * kRopePairs));
         }
     }
 }
 
-struct Row
+// rope_fixed for a run whose first pair index is a multiple of kPairs known
+// only at run time (slice = first pair / kPairs, 0 <= slice < 64 / kPairs).
+template <int kPairs>
+__device__ __forceinline__ void rope_slice(float* v, int slice, int ct, int ch, int cw, const float* table)
 {
-    bool video;
-    int t, h, w; // absolute grid position (video)
-    int k;       // text index
-    int ct, ch, cw;
-};
+    static_assert(kPairs == 4 || kPairs == 8 || kPairs == 16, "slice width");
+    switch (slice)
+    {
+#define AWA_ROPE_CASE(n)                                                            \
+    case n:                                                                         \
+        if constexpr ((n + 1) * kPairs <= 64)                                       \
+            rope_fixed<(n * kPairs) % 64, kPairs>(v, ct, ch, cw, table);            \
+        break;
+        AWA_ROPE_CASE(0)
+        AWA_ROPE_CASE(1)
+        AWA_ROPE_CASE(2)
+        AWA_ROPE_CASE(3)
+        AWA_ROPE_CASE(4)
+        AWA_ROPE_CASE(5)
+        AWA_ROPE_CASE(6)
+        AWA_ROPE_CASE(7)
+        AWA_ROPE_CASE(8)
+        AWA_ROPE_CASE(9)
+        AWA_ROPE_CASE(10)
+        AWA_ROPE_CASE(11)
+        AWA_ROPE_CASE(12)
+        AWA_ROPE_CASE(13)
+        AWA_ROPE_CASE(14)
+        AWA_ROPE_CASE(15)
+#undef AWA_ROPE_CASE
+    default:
+        break;
+    }
+}
 
-// Window-local row i -> grid position / text index and RoPE coordinates
-// (video coordinates are (T_x + t - t0, h - h0, w - w0), text (k, k, k)).
-__device__ __forceinline__ Row locate_row(const WindowDesc& win, int i, int text_tokens)
+// Row table entry of window-local row i: video rows store their local
+// (t, h, w) in 10-bit fields, text rows set bit 31 and store k.
+__device__ __forceinline__ uint32_t encode_row(const WindowDesc& win, int i)
 {
-    Row r;
     if (i < win.video_tokens)
     {
         const int area = win.eh * win.ew;
@@ -129,133 +204,354 @@ __device__ __forceinline__ Row locate_row(const WindowDesc& win, int i, int text
         const int rem = i - lt * area;
         const int lh = rem / win.ew;
         const int lw = rem - lh * win.ew;
-        r.video = true;
-        r.t = win.t0 + lt;
-        r.h = win.h0 + lh;
-        r.w = win.w0 + lw;
-        r.k = 0;
-        r.ct = text_tokens + lt;
-        r.ch = lh;
-        r.cw = lw;
+        return (static_cast<uint32_t>(lt) << 20) | (static_cast<uint32_t>(lh) << 10) | static_cast<uint32_t>(lw);
     }
-    else
-    {
-        const int k = i - win.video_tokens;
-        r.video = false;
-        r.t = r.h = r.w = 0;
-        r.k = k;
-        r.ct = r.ch = r.cw = k;
-    }
+    return 0x80000000u | static_cast<uint32_t>(i - win.video_tokens);
+}
+
+// A decoded row table entry. Both interpretations are computed and selected,
+// so rows of a wave that mix video and text take no divergent branch.
+struct RowRef
+{
+    bool text;
+    int k;          // text index
+    int t, h, w;    // grid position (video)
+    int ct, ch, cw; // RoPE coordinates
+    uint32_t token; // video token index (meaningful for video rows)
+};
+
+__device__ __forceinline__ RowRef decode_row(uint32_t e, int t0, int h0, int w0, int text_tokens, int source_h,
+                                             int source_w)
+{
+    RowRef r;
+    const int k = static_cast<int>(e & 0x7fffffffu);
+    const int lt = static_cast<int>((e >> 20) & 1023u);
+    const int lh = static_cast<int>((e >> 10) & 1023u);
+    const int lw = static_cast<int>(e & 1023u);
+    r.text = (e & 0x80000000u) != 0;
+    r.k = k;
+    r.t = t0 + lt;
+    r.h = h0 + lh;
+    r.w = w0 + lw;
+    // Unsigned arithmetic: for text rows the video fields are meaningless
+    // (and may wrap), the value is then never used.
+    r.token = (static_cast<uint32_t>(r.t) * static_cast<uint32_t>(source_h) + static_cast<uint32_t>(r.h)) *
+                  static_cast<uint32_t>(source_w) +
+              static_cast<uint32_t>(r.w);
+    r.ct = r.text ? k : text_tokens + lt;
+    r.ch = r.text ? k : lh;
+    r.cw = r.text ? k : lw;
     return r;
 }
 
-template <typename TIn>
-__device__ __forceinline__ const TIn* fused_row_ptr(const AttentionLaunch& p, const Row& r, int qkv, int head)
-{
-    if (r.video)
-    {
-        const long long token = (static_cast<long long>(r.t) * p.source_h + r.h) * p.source_w + r.w;
-        return static_cast<const TIn*>(p.video.data) + token * p.video.token_stride + qkv * p.video.qkv_stride +
-               head * kHeadDim;
-    }
-    return static_cast<const TIn*>(p.text.data) + r.k * p.text.token_stride + qkv * p.text.qkv_stride +
-           head * kHeadDim;
-}
-
-template <typename TIn>
-__device__ __forceinline__ const TIn* packed_row_ptr(const AttentionLaunch& p, int row, int qkv, int head)
-{
-    return static_cast<const TIn*>(p.packed_in) + row * p.packed_in_row + (qkv * p.heads + head) * kHeadDim;
-}
-
-// Row order of the K tile as read by the S^T MFMA: swap bits 2 and 3.
+// Row order of a 32-key block as read by the S^T MFMA: swap bits 2 and 3.
 __device__ __forceinline__ int key_permute(int m)
 {
     return (m & ~0xC) | ((m & 4) << 1) | ((m & 8) >> 1);
 }
 
-__device__ __forceinline__ void store4(float* dst, const float v[4])
+// Key swizzle of the transposed V tile: row d of Vt stores key k at column
+// k ^ (8 * vt_swizzle(d / 8)). Groups of 8 keys stay contiguous (one 16-byte
+// MFMA operand read), while the staging writes of the 16 feature chunks land
+// in distinct LDS banks.
+template <int KT>
+__device__ __forceinline__ int vt_swizzle(int chunk)
 {
-    *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+    return (chunk + (chunk >> 3)) & (KT / 8 - 1);
 }
 
-__device__ __forceinline__ void store4(uint16_t* dst, const float v[4])
+__device__ __forceinline__ void store4(float* dst, float a, float b, float c, float d)
 {
-    *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    *reinterpret_cast<float4*>(dst) = make_float4(a, b, c, d);
+}
+
+__device__ __forceinline__ void store4(uint16_t* dst, float a, float b, float c, float d)
+{
+    *reinterpret_cast<uint2*>(dst) = make_uint2(cvt_pk_bf16(a, b), cvt_pk_bf16(c, d));
+}
+
+template <typename TOut>
+__device__ __forceinline__ void store_row(TOut* dst, const f32x16 (&o)[4], float inv, int half)
+{
+#pragma unroll
+    for (int db = 0; db < 4; db++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+            store4(dst + db * 32 + 8 * g + 4 * half, o[db][4 * g] * inv, o[db][4 * g + 1] * inv,
+                   o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
 }
 
 template <typename TIn, typename TOut, bool BF16, bool FUSED>
-__global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const AttentionLaunch p)
+__global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const AttentionLaunch p)
 {
-    // LDS: K tile, transposed V tile, RoPE table.
-    constexpr int kKBytes = BF16 ? kKeyTile * kKPitchBf * 2 : kKeyTile * kKPitchF * 4;
-    constexpr int kVBytes = BF16 ? kHeadDim * kVPitchBf * 2 : kHeadDim * kVPitchF * 4;
-    __shared__ __attribute__((aligned(16))) unsigned char k_lds[kKBytes];
-    __shared__ __attribute__((aligned(16))) unsigned char v_lds[kVBytes];
-    __shared__ float rope_lds[FUSED ? kMaxRopeCoords * kRopePairs * 2 : 1];
+    // Key tile and LDS layout (pitches in elements; rows stay 16-byte aligned).
+    // 64-key tiles (two 32-key score blocks) on bf16 MFMA, 32 on fp32 MFMA.
+    constexpr int KT = BF16 ? 64 : 32;
+    constexpr int kKPitch = BF16 ? kHeadDim + 8 : kHeadDim + 4;
+    constexpr int kVPitch = BF16 ? KT + 8 : KT + 4;
+    constexpr int kElem = BF16 ? 2 : 4;
+    constexpr int kRW = kRawWords8<TIn>;
+
+    __shared__ __attribute__((aligned(16))) unsigned char k_lds[KT * kKPitch * kElem];
+    __shared__ __attribute__((aligned(16))) unsigned char v_lds[kHeadDim * kVPitch * kElem];
+    __shared__ __attribute__((aligned(16))) float rope_lds[FUSED ? kMaxRopeCoords * kRopeRow : 4];
+    extern __shared__ __attribute__((aligned(16))) unsigned char row_dyn[]; // fused: row table
 
     const WorkItem item = p.work[blockIdx.x];
     if (item.window < 0)
         return;
-    const WindowDesc win = p.windows[item.window];
-    const int head = item.head_qblock >> 16;
-    const int qblock = item.head_qblock & 0xffff;
+    const WindowDesc win = item.win;
+    const int head = item.head;
+    const int qblock = item.qblock;
     const int L = win.video_tokens + p.text_tokens;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int col = lane & 31;
     const int half = lane >> 5;
+    const int head_off = head * kHeadDim;
 
+    // Wave-uniform scalars read once from the kernel arguments (plain values,
+    // so that per-lane selects never turn into indexed struct accesses).
+    const TIn* const video_base = static_cast<const TIn*>(p.video.data);
+    const TIn* const text_base = static_cast<const TIn*>(p.text.data);
+    const long long v_tok = p.video.token_stride;
+    const long long v_qkv = p.video.qkv_stride;
+    const long long t_tok = p.text.token_stride;
+    const long long t_qkv = p.text.qkv_stride;
+    const TIn* packed_base = static_cast<const TIn*>(p.packed_in);
+    const long long packed_row = p.packed_in_row;
+    const long long packed_qkv = static_cast<long long>(p.heads) * kHeadDim;
+    const float scale_log2 = p.scale_log2;
+
+    // RoPE table: the loads are issued first and land in LDS after the
+    // Q and first-tile loads below are in flight.
+    constexpr int kRopePerThread = (kMaxRopeCoords * kRopeRow + kThreads - 1) / kThreads;
+    float rope_reg[FUSED ? kRopePerThread : 1];
     if constexpr (FUSED)
     {
-        for (int e = tid; e < p.rope_coords * kRopePairs * 2; e += kThreads)
-            rope_lds[e] = p.rope_cs[e];
-        __syncthreads();
+        const int n = p.rope_coords * kRopeRow;
+#pragma unroll
+        for (int j = 0; j < kRopePerThread; j++)
+        {
+            const int e = tid + j * kThreads;
+            rope_reg[j] = e < n ? p.rope_cs[e] : 0.f;
+        }
     }
+
+    // Row table (fused mode, LDS): for every window row the element offset of
+    // (row, qkv 0, head 0) in its blob, bit 63 marking text rows, and its RoPE
+    // coordinates packed as ct | ch << 8 | cw << 16 (all below 128).
+    unsigned long long* row_off = reinterpret_cast<unsigned long long*>(row_dyn);
+    uint32_t* row_code = reinterpret_cast<uint32_t*>(row_off + p.max_window_tokens);
+
+    // Pointer to (row i, qkv, head). Rows past the window end are clamped to
+    // its last row: their keys are masked and their values weighted by zero,
+    // so every load is in bounds and unconditional.
+    auto row_src = [&](int i, int qkv) -> const TIn* {
+        i = min(i, L - 1);
+        if constexpr (FUSED)
+        {
+            const unsigned long long off = row_off[i];
+            const long long e = static_cast<long long>(off & 0x7fffffffffffffffull);
+            const TIn* vb = video_base + qkv * v_qkv;
+            const TIn* tb = text_base + qkv * t_qkv;
+            return ((off >> 63) ? tb : vb) + e + head_off;
+        }
+        else
+        {
+            return packed_base + (win.seq_start + i) * packed_row + qkv * packed_qkv + head_off;
+        }
+    };
+    auto row_coords = [&](int i, int& ct, int& ch, int& cw) {
+        const uint32_t code = row_code[min(i, L - 1)];
+        ct = static_cast<int>(code & 255u);
+        ch = static_cast<int>((code >> 8) & 255u);
+        cw = static_cast<int>((code >> 16) & 255u);
+    };
 
     const int wave_row0 = qblock * kQueryRows + wave * 32;
     const bool wave_active = wave_row0 < L;
     const int qi = wave_row0 + col;
     const bool q_valid = qi < L;
 
-    // ---- Q into registers (B operand of S^T = K Q^T) ----
+    // ---- staging assignment ----
+    // Loads are coalesced: 16 consecutive threads read the 16 chunks of 8
+    // features of one row, so each load instruction covers 4 whole rows.
+    // Thread tid owns chunk kc = tid % 16 of K rows kr0 + 32 j and of V key
+    // group kr0: keys 2 kr0, 2 kr0 + 1 for bf16 MFMA (one 32-bit word of the
+    // transposed tile), key kr0 for fp32 MFMA.
+    constexpr int kKRows = KT / 32;
+    constexpr int kVKeys = BF16 ? 2 : 1;
+    static_assert(KT / kVKeys == 32, "32 V key groups per tile");
+    const int kc = tid & 15;
+    const int kr0 = tid >> 4;
+    // RoPE of this thread's feature pairs 4kc .. 4kc+3: the coordinate of pair
+    // q is byte rope_shift[q] / 8 of the row's coordinate word (byte 3 names
+    // the identity row: unrotated features 126, 127), and rope_col[q] is its
+    // column in the table.
+    int rope_shift[4], rope_col[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+    {
+        const int pair = 4 * kc + q;
+        const int axis = 2 * pair < kRopeDim ? pair / kRopePairs : 3;
+        rope_shift[q] = 8 * axis;
+        rope_col[q] = axis < 3 ? 2 * (pair - axis * kRopePairs) : 0;
+    }
+
+    // Two register stages: the loads of tile t+2 are issued while tile t is
+    // computed, so two tiles' loads are always in flight.
+    struct Stage
+    {
+        uint32_t k[kKRows * kRW];
+        uint32_t v[kVKeys * kRW];
+    };
+    Stage st0, st1;
+
+    auto load_tile = [&](int tile, Stage& st) {
+#pragma unroll
+        for (int j = 0; j < kKRows; j++)
+            load_raw8(row_src(tile * KT + kr0 + 32 * j, 1) + 8 * kc, st.k + j * kRW);
+#pragma unroll
+        for (int j = 0; j < kVKeys; j++)
+            load_raw8(row_src(tile * KT + kVKeys * kr0 + j, 2) + 8 * kc, st.v + j * kRW);
+    };
+
+    auto store_tile = [&](int tile, const Stage& st) {
+#pragma unroll
+        for (int j = 0; j < kKRows; j++)
+        {
+            const int row = kr0 + 32 * j;
+            float kv[8];
+            raw_to_float8<TIn>(st.k + j * kRW, kv);
+            if constexpr (FUSED)
+            {
+                const uint32_t code = row_code[min(tile * KT + row, L - 1)];
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                {
+                    const uint32_t coord = (code >> rope_shift[q]) & 255u;
+                    const float2 t = *reinterpret_cast<const float2*>(rope_lds + coord * kRopeRow + rope_col[q]);
+                    if constexpr (BF16)
+                        rope_pair_fma(kv[2 * q], kv[2 * q + 1], t.x, t.y);
+                    else
+                        rope_pair_cs(kv[2 * q], kv[2 * q + 1], t.x, t.y);
+                }
+            }
+            if constexpr (BF16)
+            {
+                uint16_t* ks = reinterpret_cast<uint16_t*>(k_lds) + row * kKPitch + 8 * kc;
+                *reinterpret_cast<uint4*>(ks) = make_uint4(cvt_pk_bf16(kv[0], kv[1]), cvt_pk_bf16(kv[2], kv[3]),
+                                                           cvt_pk_bf16(kv[4], kv[5]), cvt_pk_bf16(kv[6], kv[7]));
+            }
+            else
+            {
+                float* ks = reinterpret_cast<float*>(k_lds) + row * kKPitch + 8 * kc;
+                *reinterpret_cast<float4*>(ks) = make_float4(kv[0], kv[1], kv[2], kv[3]);
+                *reinterpret_cast<float4*>(ks + 4) = make_float4(kv[4], kv[5], kv[6], kv[7]);
+            }
+        }
+        // V transposed: Vt[d][key], keys swizzled in groups of 8 per feature chunk.
+        const int key = (kVKeys * kr0) ^ (8 * vt_swizzle<KT>(kc));
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+        {
+            if constexpr (BF16)
+            {
+                // One word = (key, key+1) at feature 8kc + e.
+                const uint32_t* a = st.v;
+                const uint32_t* b = st.v + kRW;
+                uint32_t word;
+                if constexpr (sizeof(TIn) == 2)
+                    word = __builtin_amdgcn_perm(b[e >> 1], a[e >> 1], (e & 1) ? 0x07060302u : 0x05040100u);
+                else
+                    word = cvt_pk_bf16(__uint_as_float(a[e]), __uint_as_float(b[e]));
+                *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(v_lds) + (8 * kc + e) * kVPitch + key) = word;
+            }
+            else
+            {
+                float v;
+                if constexpr (sizeof(TIn) == 2)
+                    v = (e & 1) ? bf16_hi(st.v[e >> 1]) : bf16_lo(st.v[e >> 1]);
+                else
+                    v = __uint_as_float(st.v[e]);
+                reinterpret_cast<float*>(v_lds)[(8 * kc + e) * kVPitch + key] = v;
+            }
+        }
+    };
+
+    const int tiles = (L + KT - 1) / KT;
+
+    // ---- prologue: row table (ALU only) while the RoPE table's loads are in
+    // flight; then Q and the first two tiles' loads; then the RoPE table
+    // reaches LDS ----
+    if constexpr (FUSED)
+    {
+        for (int i = tid; i < L; i += kThreads)
+        {
+            const RowRef r =
+                decode_row(encode_row(win, i), win.t0, win.h0, win.w0, p.text_tokens, p.source_h, p.source_w);
+            row_off[i] = r.text ? (0x8000000000000000ull | static_cast<unsigned long long>(r.k * t_tok))
+                                : static_cast<unsigned long long>(static_cast<long long>(r.token) * v_tok);
+            // Byte 3 names the identity row of the RoPE table (unrotated pairs).
+            row_code[i] = static_cast<uint32_t>(r.ct) | (static_cast<uint32_t>(r.ch) << 8) |
+                          (static_cast<uint32_t>(r.cw) << 16) | (static_cast<uint32_t>(p.rope_coords) << 24);
+        }
+        __syncthreads();
+    }
+    const TIn* q_src = row_src(qi, 0);
+    uint32_t qraw[8 * kRW];
+#pragma unroll
+    for (int c = 0; c < 8; c++)
+        load_raw8(q_src + (BF16 ? 16 * c + 8 * half : 64 * half + 8 * c), qraw + c * kRW);
+    load_tile(0, st0);
+    // With fp32 inputs the raw Q registers are twice as large; the second
+    // tile then follows once Q has been converted.
+    constexpr bool kEarlySecondTile = sizeof(TIn) == 2;
+    if (kEarlySecondTile && tiles > 1)
+        load_tile(1, st1);
+    int q_ct = 0, q_ch = 0, q_cw = 0;
+    if constexpr (FUSED)
+    {
+        row_coords(qi, q_ct, q_ch, q_cw);
+        const int n = p.rope_coords * kRopeRow;
+#pragma unroll
+        for (int j = 0; j < kRopePerThread; j++)
+        {
+            const int e = tid + j * kThreads;
+            if (e < n)
+                rope_lds[e] = rope_reg[j];
+        }
+        // Identity row after the last coordinate: (cos, sin) = (1, 0).
+        if (tid < kRopeRow)
+            rope_lds[n + tid] = (tid & 1) ? 0.f : 1.f;
+        __syncthreads();
+    }
+
+    // ---- Q into registers (B operand of S^T = K Q^T), scaled by log2(e)/sqrt(d) ----
     // bf16: lane holds features 16c + 8*half + [0,8) for c = 0..7.
     // fp32: lane holds features 64*half + [0,64).
     bf16x8 qb[BF16 ? 8 : 1];
     float qf[BF16 ? 1 : 64];
     {
-        const TIn* src = nullptr;
-        Row r{};
-        if (q_valid)
-        {
-            if constexpr (FUSED)
-            {
-                r = locate_row(win, qi, p.text_tokens);
-                src = fused_row_ptr<TIn>(p, r, 0, head);
-            }
-            else
-            {
-                src = packed_row_ptr<TIn>(p, win.seq_start + qi, 0, head);
-            }
-        }
+        const int ct = q_ct, ch = q_ch, cw = q_cw;
 #pragma unroll
         for (int c = 0; c < 8; c++)
         {
-            const int f0 = BF16 ? 16 * c + 8 * half : 64 * half + 8 * c;
             float v[8];
-            if (q_valid)
+            raw_to_float8<TIn>(qraw + c * kRW, v);
+            if constexpr (FUSED)
             {
-                load8(src + f0, v);
-                if constexpr (FUSED)
-                    rope8(v, f0, r.ct, r.ch, r.cw, rope_lds);
+                // 4 pairs from pair 8c + 4*half (bf16) or 32*half + 4c (fp32).
+                if constexpr (BF16)
+                    rope_slice<4>(v, 2 * c + half, ct, ch, cw, rope_lds);
+                else
+                    rope_slice<4>(v, 8 * half + c, ct, ch, cw, rope_lds);
             }
-            else
-            {
 #pragma unroll
-                for (int e = 0; e < 8; e++)
-                    v[e] = 0.f;
-            }
+            for (int e = 0; e < 8; e++)
+                v[e] *= scale_log2;
             if constexpr (BF16)
             {
                 bf16x8 x;
@@ -273,98 +569,8 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
         }
     }
 
-    // ---- staging assignment ----
-    // K: thread -> (row kr, 16 features from 16*kc); V: thread -> (keys 2*vp, 2*vp+1; features 8*vj..).
-    const int kr = tid >> 3;
-    const int kc = tid & 7;
-    const int vp = tid & 15;
-    const int vj = tid >> 4;
-    float kreg[16];
-    float vreg[16];
-
-    auto load_tile = [&](int tile) {
-        const int key = tile * kKeyTile + kr;
-        if (key < L)
-        {
-            const TIn* src;
-            if constexpr (FUSED)
-            {
-                const Row r = locate_row(win, key, p.text_tokens);
-                src = fused_row_ptr<TIn>(p, r, 1, head);
-                load8(src + 16 * kc, kreg);
-                load8(src + 16 * kc + 8, kreg + 8);
-                rope8(kreg, 16 * kc, r.ct, r.ch, r.cw, rope_lds);
-                rope8(kreg + 8, 16 * kc + 8, r.ct, r.ch, r.cw, rope_lds);
-            }
-            else
-            {
-                src = packed_row_ptr<TIn>(p, win.seq_start + key, 1, head);
-                load8(src + 16 * kc, kreg);
-                load8(src + 16 * kc + 8, kreg + 8);
-            }
-        }
-        else
-        {
-#pragma unroll
-            for (int e = 0; e < 16; e++)
-                kreg[e] = 0.f;
-        }
-#pragma unroll
-        for (int s = 0; s < 2; s++)
-        {
-            const int vkey = tile * kKeyTile + 2 * vp + s;
-            if (vkey < L)
-            {
-                const TIn* src;
-                if constexpr (FUSED)
-                    src = fused_row_ptr<TIn>(p, locate_row(win, vkey, p.text_tokens), 2, head);
-                else
-                    src = packed_row_ptr<TIn>(p, win.seq_start + vkey, 2, head);
-                load8(src + 8 * vj, vreg + 8 * s);
-            }
-            else
-            {
-#pragma unroll
-                for (int e = 0; e < 8; e++)
-                    vreg[8 * s + e] = 0.f;
-            }
-        }
-    };
-
-    auto store_tile = [&]() {
-        if constexpr (BF16)
-        {
-            uint16_t* ks = reinterpret_cast<uint16_t*>(k_lds);
-            uint16_t* vt = reinterpret_cast<uint16_t*>(v_lds);
-            uint4 a, b;
-            a.x = pack_bf16x2(kreg[0], kreg[1]);
-            a.y = pack_bf16x2(kreg[2], kreg[3]);
-            a.z = pack_bf16x2(kreg[4], kreg[5]);
-            a.w = pack_bf16x2(kreg[6], kreg[7]);
-            b.x = pack_bf16x2(kreg[8], kreg[9]);
-            b.y = pack_bf16x2(kreg[10], kreg[11]);
-            b.z = pack_bf16x2(kreg[12], kreg[13]);
-            b.w = pack_bf16x2(kreg[14], kreg[15]);
-            *reinterpret_cast<uint4*>(ks + kr * kKPitchBf + 16 * kc) = a;
-            *reinterpret_cast<uint4*>(ks + kr * kKPitchBf + 16 * kc + 8) = b;
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-                *reinterpret_cast<uint32_t*>(vt + (8 * vj + e) * kVPitchBf + 2 * vp) =
-                    pack_bf16x2(vreg[e], vreg[8 + e]);
-        }
-        else
-        {
-            float* ks = reinterpret_cast<float*>(k_lds);
-            float* vt = reinterpret_cast<float*>(v_lds);
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-                *reinterpret_cast<float4*>(ks + kr * kKPitchF + 16 * kc + 4 * q) =
-                    make_float4(kreg[4 * q], kreg[4 * q + 1], kreg[4 * q + 2], kreg[4 * q + 3]);
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-                *reinterpret_cast<float2*>(vt + (8 * vj + e) * kVPitchF + 2 * vp) = make_float2(vreg[e], vreg[8 + e]);
-        }
-    };
+    if (!kEarlySecondTile && tiles > 1)
+        load_tile(1, st1);
 
     f32x16 o[4];
 #pragma unroll
@@ -372,98 +578,118 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
 #pragma unroll
         for (int i = 0; i < 16; i++)
             o[db][i] = 0.f;
-    float row_max = -INFINITY; // log2 domain
-    float row_sum = 0.f;       // partial over this lane's keys
+    float row_max = -INFINITY; // running maximum (log2 domain), possibly stale by < 2^8
+    float row_sum = 0.f;       // partial sum over this lane's keys
 
-    const int tiles = (L + kKeyTile - 1) / kKeyTile;
-    load_tile(0);
-    for (int tile = 0; tile < tiles; tile++)
-    {
-        store_tile();
-        __syncthreads();
-        if (tile + 1 < tiles)
-            load_tile(tile + 1);
-
+    const int krow = key_permute(col);
+    auto compute_tile = [&](int tile) {
         if (wave_active)
         {
-            // ---- S^T = K Q^T (32 keys x 32 queries) ----
-            f32x16 s;
+            constexpr int kBlocks = KT / 32; // 32-key blocks in this tile
+            f32x16 s[kBlocks];
 #pragma unroll
-            for (int i = 0; i < 16; i++)
-                s[i] = 0.f;
-            const int krow = key_permute(col);
+            for (int b = 0; b < kBlocks; b++)
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    s[b][i] = 0.f;
+            // ---- S^T = K Q^T: one 32x32 block per 32 keys; chains interleaved ----
             if constexpr (BF16)
             {
-                const uint16_t* ks = reinterpret_cast<const uint16_t*>(k_lds) + krow * kKPitchBf + 8 * half;
+                const uint16_t* ks = reinterpret_cast<const uint16_t*>(k_lds) + krow * kKPitch + 8 * half;
+                bf16x8 ka[kBlocks][8];
 #pragma unroll
                 for (int c = 0; c < 8; c++)
-                {
-                    const bf16x8 ka = *reinterpret_cast<const bf16x8*>(ks + 16 * c);
-                    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qb[c], s, 0, 0, 0);
-                }
+#pragma unroll
+                    for (int b = 0; b < kBlocks; b++)
+                        ka[b][c] = *reinterpret_cast<const bf16x8*>(ks + b * 32 * kKPitch + 16 * c);
+#pragma unroll
+                for (int c = 0; c < 8; c++)
+#pragma unroll
+                    for (int b = 0; b < kBlocks; b++)
+                        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[b][c], qb[c], s[b], 0, 0, 0);
             }
             else
             {
-                const float* ks = reinterpret_cast<const float*>(k_lds) + krow * kKPitchF + 64 * half;
+                // One chain over this lane's 64 features (32x32x2 f32 MFMAs).
+                const float* ks = reinterpret_cast<const float*>(k_lds) + krow * kKPitch + 64 * half;
 #pragma unroll
                 for (int c4 = 0; c4 < 16; c4++)
                 {
                     const float4 ka = *reinterpret_cast<const float4*>(ks + 4 * c4);
-                    s = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.x, qf[4 * c4 + 0], s, 0, 0, 0);
-                    s = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.y, qf[4 * c4 + 1], s, 0, 0, 0);
-                    s = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.z, qf[4 * c4 + 2], s, 0, 0, 0);
-                    s = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.w, qf[4 * c4 + 3], s, 0, 0, 0);
+                    s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.x, qf[4 * c4 + 0], s[0], 0, 0, 0);
+                    s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.y, qf[4 * c4 + 1], s[0], 0, 0, 0);
+                    s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.z, qf[4 * c4 + 2], s[0], 0, 0, 0);
+                    s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.w, qf[4 * c4 + 3], s[0], 0, 0, 0);
                 }
             }
 
-            // ---- online softmax: register i holds key 16*(i/8) + 8*half + i%8 ----
-            const int key0 = tile * kKeyTile + 8 * half;
-            float tile_max = -INFINITY;
-#pragma unroll
-            for (int i = 0; i < 16; i++)
+            // ---- online softmax: register i of block b holds key 32b + 16*(i/8) + 8*half + i%8 ----
+            if (tile == tiles - 1 && (L % KT))
             {
-                const int key = key0 + 16 * (i >> 3) + (i & 7);
-                const float v = key < L ? s[i] * p.scale_log2 : -INFINITY;
-                s[i] = v;
-                tile_max = fmaxf(tile_max, v);
-            }
-            tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
-            const float new_max = fmaxf(row_max, tile_max);
-            const float alpha = exp2f(row_max - new_max);
-            row_max = new_max;
-            float psum = 0.f;
+                const int key0 = tile * KT + 8 * half;
 #pragma unroll
-            for (int i = 0; i < 16; i++)
-            {
-                s[i] = exp2f(s[i] - new_max);
-                psum += s[i];
-            }
-            row_sum = row_sum * alpha + psum;
+                for (int b = 0; b < kBlocks; b++)
 #pragma unroll
-            for (int db = 0; db < 4; db++)
+                    for (int i = 0; i < 16; i++)
+                        if (key0 + 32 * b + 16 * (i >> 3) + (i & 7) >= L)
+                            s[b][i] = -INFINITY;
+            }
+            float tile_max = s[0][0];
+#pragma unroll
+            for (int b = 0; b < kBlocks; b++)
 #pragma unroll
                 for (int i = 0; i < 16; i++)
-                    o[db][i] *= alpha;
+                    tile_max = fmaxf(tile_max, s[b][i]);
+            tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+            if (__any(tile_max > row_max + kRescaleThreshold))
+            {
+                const float new_max = fmaxf(row_max, tile_max);
+                const float alpha = __builtin_amdgcn_exp2f(row_max - new_max);
+                row_max = new_max;
+                row_sum *= alpha;
+#pragma unroll
+                for (int db = 0; db < 4; db++)
+#pragma unroll
+                    for (int i = 0; i < 16; i++)
+                        o[db][i] *= alpha;
+            }
+            float psum = 0.f;
+#pragma unroll
+            for (int b = 0; b < kBlocks; b++)
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                {
+                    s[b][i] = __builtin_amdgcn_exp2f(s[b][i] - row_max);
+                    psum += s[b][i];
+                }
+            row_sum += psum;
 
             // ---- O^T += V^T P^T ----
             if constexpr (BF16)
             {
-                bf16x8 pb0, pb1;
+                bf16x8 pb[2 * kBlocks];
 #pragma unroll
-                for (int e = 0; e < 8; e++)
-                {
-                    pb0[e] = static_cast<__bf16>(s[e]);
-                    pb1[e] = static_cast<__bf16>(s[8 + e]);
-                }
+                for (int b = 0; b < kBlocks; b++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                    {
+                        pb[2 * b][e] = static_cast<__bf16>(s[b][e]);
+                        pb[2 * b + 1][e] = static_cast<__bf16>(s[b][8 + e]);
+                    }
                 const uint16_t* vt = reinterpret_cast<const uint16_t*>(v_lds);
 #pragma unroll
                 for (int db = 0; db < 4; db++)
                 {
-                    const uint16_t* vrow = vt + (db * 32 + col) * kVPitchBf + 8 * half;
-                    const bf16x8 va0 = *reinterpret_cast<const bf16x8*>(vrow);
-                    const bf16x8 va1 = *reinterpret_cast<const bf16x8*>(vrow + 16);
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va0, pb0, o[db], 0, 0, 0);
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va1, pb1, o[db], 0, 0, 0);
+                    const int d = db * 32 + col;
+                    const uint16_t* vrow = vt + d * kVPitch;
+                    const int swz = 8 * vt_swizzle<KT>(d >> 3);
+                    bf16x8 va[2 * kBlocks];
+#pragma unroll
+                    for (int j = 0; j < 2 * kBlocks; j++)
+                        va[j] = *reinterpret_cast<const bf16x8*>(vrow + ((8 * half + 16 * j) ^ swz));
+#pragma unroll
+                    for (int j = 0; j < 2 * kBlocks; j++)
+                        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[j], pb[j], o[db], 0, 0, 0);
                 }
             }
             else
@@ -472,72 +698,67 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
 #pragma unroll
                 for (int db = 0; db < 4; db++)
                 {
-                    const float* vrow = vt + (db * 32 + col) * kVPitchF + 8 * half;
+                    const int d = db * 32 + col;
+                    const float* vrow = vt + d * kVPitch;
+                    const int swz = 8 * vt_swizzle<KT>(d >> 3);
 #pragma unroll
                     for (int g = 0; g < 4; g++)
                     {
-                        const float4 va = *reinterpret_cast<const float4*>(vrow + 16 * (g >> 1) + 4 * (g & 1));
-                        o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.x, s[4 * g + 0], o[db], 0, 0, 0);
-                        o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.y, s[4 * g + 1], o[db], 0, 0, 0);
-                        o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.z, s[4 * g + 2], o[db], 0, 0, 0);
-                        o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.w, s[4 * g + 3], o[db], 0, 0, 0);
+                        const float4 va =
+                            *reinterpret_cast<const float4*>(vrow + ((16 * (g >> 1) + 8 * half + 4 * (g & 1)) ^ swz));
+                        o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.x, s[0][4 * g + 0], o[db], 0, 0, 0);
+                        o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.y, s[0][4 * g + 1], o[db], 0, 0, 0);
+                        o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.z, s[0][4 * g + 2], o[db], 0, 0, 0);
+                        o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.w, s[0][4 * g + 3], o[db], 0, 0, 0);
                     }
                 }
             }
         }
+    };
+
+    // One key tile: stage it into LDS, then refill its registers with the
+    // tile two steps ahead while the scores and PV products are computed.
+    auto step = [&](int tile, Stage& st) {
+        store_tile(tile, st);
         __syncthreads();
+        if (tile + 2 < tiles)
+            load_tile(tile + 2, st);
+        compute_tile(tile);
+        __syncthreads();
+    };
+    for (int tile = 0; tile < tiles; tile += 2)
+    {
+        step(tile, st0);
+        if (tile + 1 < tiles)
+            step(tile + 1, st1);
     }
 
     if (!q_valid)
         return;
-    const float total = row_sum + __shfl_xor(row_sum, 32);
-    const float inv = 1.f / total;
+    const float inv = 1.f / (row_sum + __shfl_xor(row_sum, 32));
 
     // ---- store: lane holds features db*32 + 8*g + 4*half + [0,4) ----
     if constexpr (FUSED)
     {
-        const Row r = locate_row(win, qi, p.text_tokens);
-        if (r.video)
+        const RowRef r =
+            decode_row(encode_row(win, qi), win.t0, win.h0, win.w0, p.text_tokens, p.source_h, p.source_w);
+        if (!r.text)
         {
             TOut* dst = static_cast<TOut*>(p.video_out.data) + r.t * p.video_out.ts + r.h * p.video_out.hs +
-                        r.w * p.video_out.ws + head * kHeadDim;
-#pragma unroll
-            for (int db = 0; db < 4; db++)
-#pragma unroll
-                for (int g = 0; g < 4; g++)
-                {
-                    const float v[4] = {o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv,
-                                        o[db][4 * g + 3] * inv};
-                    store4(dst + db * 32 + 8 * g + 4 * half, v);
-                }
+                        r.w * p.video_out.ws + head_off;
+            store_row(dst, o, inv, half);
         }
         else
         {
             float* dst = p.text_partials +
                          ((static_cast<long long>(item.window) * p.text_tokens + r.k) * p.heads + head) * kHeadDim;
-#pragma unroll
-            for (int db = 0; db < 4; db++)
-#pragma unroll
-                for (int g = 0; g < 4; g++)
-                {
-                    const float v[4] = {o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv,
-                                        o[db][4 * g + 3] * inv};
-                    store4(dst + db * 32 + 8 * g + 4 * half, v);
-                }
+            store_row(dst, o, inv, half);
         }
     }
     else
     {
-        float* dst = p.packed_out + (win.seq_start + qi) * p.packed_out_row + head * kHeadDim;
-#pragma unroll
-        for (int db = 0; db < 4; db++)
-#pragma unroll
-            for (int g = 0; g < 4; g++)
-            {
-                const float v[4] = {o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv,
-                                    o[db][4 * g + 3] * inv};
-                store4(dst + db * 32 + 8 * g + 4 * half, v);
-            }
+        float* dst = p.packed_out + (win.seq_start + qi) * p.packed_out_row + head_off;
+        store_row(dst, o, inv, half);
     }
 }
 
@@ -546,8 +767,10 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
 template <typename TIn, typename TOut, bool BF16, bool FUSED>
 static hipError_t launch_one(const AttentionLaunch& p, hipStream_t stream)
 {
-    hipLaunchKernelGGL((window_attention_kernel<TIn, TOut, BF16, FUSED>), dim3(p.work_count), dim3(kThreads), 0,
-                       stream, p);
+    // Row table: one 64-bit offset and one 32-bit coordinate word per row.
+    const size_t row_table = FUSED ? static_cast<size_t>(p.max_window_tokens) * 12 : 0;
+    hipLaunchKernelGGL((window_attention_kernel<TIn, TOut, BF16, FUSED>), dim3(p.work_count), dim3(kThreads),
+                       row_table, stream, p);
     return hipGetLastError();
 }
 

@@ -179,12 +179,12 @@ std::vector<awa::WorkItem> build_work(const awa_plan& plan, int heads)
         const int x = static_cast<int>(std::min_element(load.begin(), load.end()) - load.begin());
         load[x] += u.cost;
         for (int q = 0; q < u.qblocks; q++)
-            lists[x].push_back({u.window, (u.head << 16) | q});
+            lists[x].push_back({plan.window_descs[u.window], u.window, u.head, q, 0});
     }
     size_t longest = 0;
     for (const auto& l : lists)
         longest = std::max(longest, l.size());
-    std::vector<awa::WorkItem> work(longest * kXcds, awa::WorkItem{-1, 0});
+    std::vector<awa::WorkItem> work(longest * kXcds, awa::WorkItem{awa::WindowDesc{}, -1, 0, 0, 0});
     for (int x = 0; x < kXcds; x++)
         for (size_t j = 0; j < lists[x].size(); j++)
             work[j * kXcds + x] = lists[x][j];
@@ -600,8 +600,14 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
         return fail(AWA_ERR_INVALID, "invalid QKV input blobs");
     if (vl.head_dim != awa::kHeadDim || plan->rope_dim != awa::kRopeDim)
         return fail(AWA_ERR_INVALID, "fused path needs head_dim 128 and rope_dim 126; use the staged entry points");
-    if (plan->rope_coords > awa::kMaxRopeCoords)
+    // The kernel appends an identity row after the last coordinate.
+    if (plan->rope_coords + 1 > awa::kMaxRopeCoords)
         return fail(AWA_ERR_INVALID, "RoPE coordinate range exceeds the fused kernel's table");
+    // Row table entries hold window-local coordinates in 10-bit fields, and
+    // the table itself lives in LDS next to the K/V tiles.
+    if (plan->window_t >= 1024 || plan->window_h >= 1024 || plan->window_w >= 1024 ||
+        plan->max_window_tokens > awa::kMaxFusedWindowTokens)
+        return fail(AWA_ERR_INVALID, "window too large for the fused kernel; use the staged entry points");
     const int elem = video_qkv->elemsize;
     const int align_elems = 16 / elem;
     if (!aligned16(video_qkv->data) || !aligned16(text_qkv->data) || vl.token_stride % align_elems ||
@@ -634,6 +640,7 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
     p.work_count = plan->work_count;
     p.rope_cs = plan->dev.rope_cs;
     p.rope_coords = plan->rope_coords;
+    p.max_window_tokens = plan->max_window_tokens;
     p.heads = vl.heads;
     p.text_tokens = plan->text_tokens;
     p.source_h = plan->source_h;

@@ -11,8 +11,10 @@ namespace awa
 
 constexpr int kHeadDim = 128;   // head_dim of the MFMA attention kernels
 constexpr int kRopeDim = 126;   // rope_dim of the fused kernel
-constexpr int kQueryRows = 128; // query rows per workgroup (4 waves x 32)
+constexpr int kQueryWaves = 8;  // waves per attention workgroup, 32 query rows each
+constexpr int kQueryRows = 32 * kQueryWaves; // query rows per workgroup
 constexpr int kMaxRopeCoords = 128; // RoPE coordinates the fused kernel holds in LDS
+constexpr int kMaxFusedWindowTokens = 1536; // rows of the fused kernel's LDS row table
 
 // One QKV source: row of (token, qkv, head) starts at
 // token * token_stride + qkv * qkv_stride + head * head_dim.
@@ -52,6 +54,7 @@ struct AttentionLaunch
     int work_count;
     const float* rope_cs;
     int rope_coords;
+    int max_window_tokens; // rows of the largest window (fused-mode LDS row table)
     int heads;
     int text_tokens;
     int source_h, source_w;

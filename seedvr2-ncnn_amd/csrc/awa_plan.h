@@ -28,12 +28,16 @@ struct alignas(16) WindowDesc
     int seq_start;
 };
 
-// One workgroup's share of the fused / packed attention: window, head and the
-// first query row of its query block. window < 0 marks padding.
-struct alignas(8) WorkItem
+// One workgroup's share of the fused / packed attention: the window (its
+// descriptor is embedded so that a workgroup needs a single dependent load to
+// start), the head and the query block. window < 0 marks padding.
+struct alignas(16) WorkItem
 {
+    WindowDesc win;
     int window;
-    int head_qblock; // head << 16 | query block
+    int head;
+    int qblock;
+    int reserved;
 };
 
 // Packed-row descriptor for the staged kernels: source row (video index, or
