@@ -86,8 +86,12 @@ def main() -> int:
     ap.add_argument("--profile-steps", type=int, default=5, help="steps with per-block event timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-layers", type=int, default=2, choices=(1, 2))
-    ap.add_argument("--traffic-json", default=None,
-                    help="JSON with measured HBM bytes per launch of the dominant kernel (from rocprofv3 --pmc)")
+    ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "awa_attention_hbm_traffic.json"),
+                    help="measured HBM bytes per launch of each attention kernel (rocprofv3 --pmc FETCH_SIZE and "
+                         "WRITE_SIZE, scaled by the copy calibration)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 5 plain 64 MiB fp32 device copies (awa_cast), the known-size reference the "
+                         "FETCH_SIZE / WRITE_SIZE counters are scaled by, and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -97,6 +101,16 @@ def main() -> int:
     import awa_hip as A
 
     A.init(0)
+    if args.copy_calibration:
+        n = 64 * 1024 * 1024 // 4
+        src, dst = A.DeviceBuffer(n * 4), A.DeviceBuffer(n * 4)
+        src.fill_normal(n, 4, 3)
+        bi, bo = A.mat(src.ptr, 1024, 1024, 16, 4), A.mat(dst.ptr, 1024, 1024, 16, 4)
+        for _ in range(5):
+            A.cast(bi, bo)
+        A.synchronize()
+        print("copy calibration: 5 x 64 MiB fp32 device copies (read 64 MiB + write 64 MiB each)", flush=True)
+        return 0
     t, h, w = GRID
     N = t * h * w
     row_qkv = 3 * HEADS * HEAD_DIM
@@ -159,7 +173,9 @@ def main() -> int:
     traffic = None
     if args.traffic_json and os.path.exists(args.traffic_json):
         with open(args.traffic_json) as f:
-            traffic = json.load(f).get("bytes_per_launch")
+            entry = json.load(f).get("kernels", {}).get("bf16" if dom is bf16_idx else "fp32")
+        if entry is not None:
+            traffic = entry.get("hbm_bytes_per_launch")
 
     def layer_stats(idx):
         ms = float(att[idx].mean())
