@@ -137,6 +137,11 @@ int awa_plan_upload(awa_plan* plan, void* stream);
 
 /* ---- forward entry points ---- */
 
+/* Heads and head_dim of a QKV blob over `tokens` tokens in one of the four
+ * accepted layouts (describe_qkv_layout, src/awa/awa_layers.cpp:116-182);
+ * -1 when the blob matches none. Host-only: reads the descriptor, not data. */
+int awa_qkv_shape(const awa_blob* qkv, int tokens, int* heads, int* head_dim);
+
 /* Fused layer: gather + MMRoPE + window attention + scatter + text mean in one
  * pass, equivalent to Pack -> MMRoPE -> WindowAttention -> Unpack.
  * video_qkv: the four QKV layouts of describe_qkv_layout (src/awa/awa_layers.cpp:116-170)

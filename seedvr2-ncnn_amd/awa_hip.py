@@ -34,7 +34,7 @@ EXPORTED_SYMBOLS = (
     "awa_event_synchronize", "awa_event_elapsed_ms", "awa_fill_normal", "awa_plan_create", "awa_plan_destroy",
     "awa_plan_info_get", "awa_plan_windows", "awa_plan_sequence_index", "awa_plan_cu_seqlens",
     "awa_plan_video_positions", "awa_plan_text_positions", "awa_plan_rope_table", "awa_plan_upload",
-    "awa_forward", "awa_pack", "awa_mmrope", "awa_window_attention", "awa_unpack", "awa_cast",
+    "awa_qkv_shape", "awa_forward", "awa_pack", "awa_mmrope", "awa_window_attention", "awa_unpack", "awa_cast",
     "awa_stack_create", "awa_stack_destroy", "awa_stack_run", "awa_stack_set_profiling", "awa_stack_block_times",
     "awa_stack_block_flops",
 )

@@ -659,6 +659,18 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
 
 extern "C" {
 
+int awa_qkv_shape(const awa_blob* qkv, int tokens, int* heads, int* head_dim)
+{
+    if (!qkv || !heads || !head_dim || tokens <= 0)
+        return fail(AWA_ERR_INVALID, "null argument");
+    QkvLayout l;
+    if (!describe_qkv(*qkv, tokens, l))
+        return fail(AWA_ERR_INVALID, "blob matches none of the QKV layouts");
+    *heads = l.heads;
+    *head_dim = l.head_dim;
+    return AWA_OK;
+}
+
 int awa_pack(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv, const awa_blob* packed,
              const awa_blob* cu_seqlens, void* stream)
 {

@@ -1,0 +1,538 @@
+// C++ operator surface of the AWA path over the C ABI (see awa_layers.h).
+// Layer semantics follow src/awa/awa_layers.cpp: params (:90-114, :867-874),
+// construction flags (:363-373, :581-590, :849-858, :1028-1037), registration
+// (:1237-1291); the device work is the C ABI's.
+#include "awa_layers.h"
+
+#include <cstdio>
+#include <limits>
+
+namespace seedvr2
+{
+
+bool AwaRuntimeSpec::valid() const
+{
+    const long long computed = static_cast<long long>(source_t) * source_h * source_w;
+    return source_t > 0 && source_h > 0 && source_w > 0 && video_tokens > 0 && computed == video_tokens &&
+           computed <= std::numeric_limits<int>::max();
+}
+
+std::vector<AwaWindow> make_awa_windows(int source_t, int source_h, int source_w, int windows_t, int windows_h,
+                                        int windows_w, bool shifted)
+{
+    awa_plan_desc desc{};
+    desc.source_t = source_t;
+    desc.source_h = source_h;
+    desc.source_w = source_w;
+    desc.windows_t = windows_t;
+    desc.windows_h = windows_h;
+    desc.windows_w = windows_w;
+    desc.text_tokens = 1; // the partition does not depend on the text length
+    desc.shifted = shifted ? 1 : 0;
+    if (source_t <= 0 || source_h <= 0 || source_w <= 0)
+        return {};
+    awa_plan* plan = nullptr;
+    if (awa_plan_create(&desc, &plan) != AWA_OK)
+        return {};
+    awa_plan_info info{};
+    std::vector<AwaWindow> result;
+    if (awa_plan_info_get(plan, &info) == AWA_OK)
+    {
+        std::vector<int> boxes(static_cast<size_t>(info.window_count) * 6);
+        if (awa_plan_windows(plan, boxes.data()) == AWA_OK)
+            for (int i = 0; i < info.window_count; i++)
+            {
+                const int* b = &boxes[static_cast<size_t>(i) * 6];
+                result.push_back({b[0], b[1], b[2], b[3], b[4], b[5]});
+            }
+    }
+    awa_plan_destroy(plan);
+    return result;
+}
+
+namespace hip
+{
+
+namespace
+{
+
+class DeviceAllocator final : public Allocator
+{
+public:
+    void* fastMalloc(size_t size) override
+    {
+        void* ptr = nullptr;
+        return awa_malloc(&ptr, size) == AWA_OK ? ptr : nullptr;
+    }
+    void fastFree(void* ptr) override { awa_free(ptr); }
+};
+
+long long align16_elements(long long elements, size_t elemsize)
+{
+    const long long bytes = elements * static_cast<long long>(elemsize);
+    return ((bytes + 15) / 16 * 16) / static_cast<long long>(elemsize);
+}
+
+} // namespace
+
+Allocator* default_device_allocator()
+{
+    static DeviceAllocator allocator;
+    return &allocator;
+}
+
+int Mat::allocate(Allocator* allocator)
+{
+    Allocator* a = allocator ? allocator : default_device_allocator();
+    const size_t bytes = static_cast<size_t>(total()) * elemsize;
+    void* ptr = bytes ? a->fastMalloc(bytes) : nullptr;
+    if (bytes && !ptr)
+    {
+        release();
+        return AWA_ERR_ALLOC;
+    }
+    storage_ = std::shared_ptr<void>(ptr, [a](void* p) {
+        if (p)
+            a->fastFree(p);
+    });
+    data = ptr;
+    return AWA_OK;
+}
+
+int Mat::create(int w_, size_t elemsize_, Allocator* allocator)
+{
+    release();
+    dims = 1;
+    w = w_;
+    h = d = c = n = 1;
+    elemsize = elemsize_;
+    cstep = nstep = w_;
+    return allocate(allocator);
+}
+
+int Mat::create(int w_, int h_, int c_, size_t elemsize_, Allocator* allocator, int n_)
+{
+    release();
+    dims = 3;
+    w = w_;
+    h = h_;
+    d = 1;
+    c = c_;
+    n = n_;
+    elemsize = elemsize_;
+    cstep = align16_elements(static_cast<long long>(w_) * h_, elemsize_);
+    // Batches of the NCNN_BATCH layout start on 4 KiB boundaries (src/awa/awa_layers.cpp:537-539).
+    nstep = n_ > 1 ? (static_cast<long long>((cstep * c_ * static_cast<long long>(elemsize_) + 4095) / 4096 * 4096) /
+                      static_cast<long long>(elemsize_))
+                   : cstep * c_;
+    return allocate(allocator);
+}
+
+int Mat::create_4d(int w_, int h_, int d_, int c_, size_t elemsize_, Allocator* allocator, int n_)
+{
+    release();
+    dims = 4;
+    w = w_;
+    h = h_;
+    d = d_;
+    c = c_;
+    n = n_;
+    elemsize = elemsize_;
+    cstep = align16_elements(static_cast<long long>(w_) * h_ * d_, elemsize_);
+    nstep = n_ > 1 ? (static_cast<long long>((cstep * c_ * static_cast<long long>(elemsize_) + 4095) / 4096 * 4096) /
+                      static_cast<long long>(elemsize_))
+                   : cstep * c_;
+    return allocate(allocator);
+}
+
+void Mat::release()
+{
+    storage_.reset();
+    data = nullptr;
+    dims = 0;
+    w = h = 0;
+    d = c = n = 1;
+    cstep = nstep = 0;
+}
+
+awa_blob Mat::blob() const
+{
+    awa_blob b{};
+    b.data = data;
+    b.dims = dims;
+    b.w = w;
+    b.h = h;
+    b.d = d;
+    b.c = c;
+    b.n = n;
+    b.elemsize = static_cast<int>(elemsize);
+    b.cstep = cstep;
+    b.nstep = nstep;
+    return b;
+}
+
+Mat Mat::external(const awa_blob& b)
+{
+    Mat m;
+    m.data = b.data;
+    m.dims = b.dims;
+    m.w = b.w;
+    m.h = b.h;
+    m.d = b.d;
+    m.c = b.c;
+    m.n = b.n;
+    m.elemsize = static_cast<size_t>(b.elemsize);
+    m.cstep = b.cstep;
+    m.nstep = b.nstep;
+    return m;
+}
+
+int ParamDict::get(int id, int default_value) const
+{
+    const auto it = values_.find(id);
+    return it == values_.end() ? default_value : it->second;
+}
+
+void ParamDict::set(int id, int value)
+{
+    values_[id] = value;
+}
+
+int Layer::load_param(const ParamDict&)
+{
+    return 0;
+}
+
+int Layer::upload_model(const Option&)
+{
+    return 0;
+}
+
+int Layer::create_pipeline(const Option&)
+{
+    return 0;
+}
+
+int Layer::destroy_pipeline(const Option&)
+{
+    return 0;
+}
+
+int Layer::forward(const std::vector<Mat>&, std::vector<Mat>&, const Option&) const
+{
+    return -1;
+}
+
+int Net::register_custom_layer(const char* type, layer_creator_func creator, layer_destroyer_func, void* userdata)
+{
+    if (!type || !creator)
+        return -1;
+    registry_[type] = Entry{creator, userdata};
+    return 0;
+}
+
+std::unique_ptr<Layer> Net::create_custom_layer(const char* type) const
+{
+    const auto it = type ? registry_.find(type) : registry_.end();
+    if (it == registry_.end())
+        return nullptr;
+    return std::unique_ptr<Layer>(it->second.creator(it->second.userdata));
+}
+
+std::vector<std::string> Net::custom_layer_types() const
+{
+    std::vector<std::string> types;
+    for (const auto& kv : registry_)
+        types.push_back(kv.first);
+    return types;
+}
+
+} // namespace hip
+} // namespace seedvr2
+
+using seedvr2::hip::Mat;
+using seedvr2::hip::Option;
+using seedvr2::hip::ParamDict;
+
+namespace
+{
+
+void report(const char* layer, int rc)
+{
+    if (rc != AWA_OK)
+        std::fprintf(stderr, "%s: %s\n", layer, awa_last_error());
+}
+
+} // namespace
+
+SeedVR2AwaLayerBase::SeedVR2AwaLayerBase(const char* type_name, bool reads_rope_dim) : reads_rope_dim_(reads_rope_dim)
+{
+    type = type_name;
+    one_blob_only = false;
+    support_inplace = false;
+}
+
+SeedVR2AwaLayerBase::SeedVR2AwaLayerBase(const char* type_name, bool reads_rope_dim,
+                                         const seedvr2::AwaRuntimeSpec& spec)
+    : SeedVR2AwaLayerBase(type_name, reads_rope_dim)
+{
+    has_runtime_spec_ = true;
+    runtime_spec_ = spec;
+}
+
+SeedVR2AwaLayerBase::~SeedVR2AwaLayerBase()
+{
+    awa_plan_destroy(plan_);
+}
+
+int SeedVR2AwaLayerBase::load_param(const ParamDict& pd)
+{
+    awa_plan_destroy(plan_);
+    plan_ = nullptr;
+    uploaded_ = false;
+    awa_plan_desc desc{};
+    desc.source_t = pd.get(0, 0);
+    desc.source_h = pd.get(1, 0);
+    desc.source_w = pd.get(2, 0);
+    desc.windows_t = pd.get(3, 0);
+    desc.windows_h = pd.get(4, 0);
+    desc.windows_w = pd.get(5, 0);
+    desc.text_tokens = pd.get(6, 0);
+    desc.shifted = pd.get(7, 0) != 0 ? 1 : 0;
+    // Only the MMRoPE layer reads param 8 (src/awa/awa_layers.cpp:872); the
+    // others build their maps with the default.
+    desc.rope_dim = reads_rope_dim_ ? pd.get(8, 126) : 126;
+    if (has_runtime_spec_)
+    {
+        desc.runtime_t = runtime_spec_.source_t;
+        desc.runtime_h = runtime_spec_.source_h;
+        desc.runtime_w = runtime_spec_.source_w;
+        desc.runtime_tokens = runtime_spec_.video_tokens;
+    }
+    const int rc = awa_plan_create(&desc, &plan_);
+    if (rc != AWA_OK)
+    {
+        plan_ = nullptr;
+        return rc;
+    }
+    return awa_plan_info_get(plan_, &info_);
+}
+
+int SeedVR2AwaLayerBase::upload_model(const Option& opt)
+{
+    if (!plan_)
+        return -1;
+    const int rc = awa_plan_upload(plan_, opt.stream);
+    report(type.c_str(), rc);
+    uploaded_ = rc == AWA_OK;
+    return rc;
+}
+
+int SeedVR2AwaLayerBase::destroy_pipeline(const Option&)
+{
+    awa_plan_destroy(plan_);
+    plan_ = nullptr;
+    uploaded_ = false;
+    return 0;
+}
+
+int SeedVR2AwaLayerBase::require_uploaded() const
+{
+    if (!plan_ || !uploaded_)
+    {
+        std::fprintf(stderr, "%s: forward before load_param/upload_model\n", type.c_str());
+        return -1;
+    }
+    return 0;
+}
+
+SeedVR2AWAPack::SeedVR2AWAPack() : SeedVR2AwaLayerBase("SeedVR2AWAPack", false)
+{
+    support_batch = true;
+}
+
+SeedVR2AWAPack::SeedVR2AWAPack(const seedvr2::AwaRuntimeSpec& spec) : SeedVR2AwaLayerBase("SeedVR2AWAPack", false, spec)
+{
+    support_batch = true;
+}
+
+int SeedVR2AWAPack::forward(const std::vector<Mat>& bottom_blobs, std::vector<Mat>& top_blobs,
+                            const Option& opt) const
+{
+    if (require_uploaded() != 0)
+        return -1;
+    if (bottom_blobs.size() != 2)
+        return -1;
+    const awa_blob video = bottom_blobs[0].blob();
+    const awa_blob text = bottom_blobs[1].blob();
+    int heads = 0, head_dim = 0;
+    int rc = awa_qkv_shape(&video, info_.source_tokens, &heads, &head_dim);
+    if (rc != AWA_OK)
+    {
+        report(type.c_str(), rc);
+        return rc;
+    }
+    top_blobs.resize(2);
+    if (top_blobs[0].create(head_dim, 3 * heads, info_.sequence_tokens, 4, opt.blob_allocator) != AWA_OK ||
+        top_blobs[1].create(info_.window_count + 1, 4, opt.blob_allocator) != AWA_OK)
+        return AWA_ERR_ALLOC;
+    const awa_blob packed = top_blobs[0].blob();
+    const awa_blob cu = top_blobs[1].blob();
+    rc = awa_pack(plan_, &video, &text, &packed, &cu, opt.stream);
+    report(type.c_str(), rc);
+    return rc;
+}
+
+SeedVR2MMRoPE::SeedVR2MMRoPE() : SeedVR2AwaLayerBase("SeedVR2MMRoPE", true)
+{
+}
+
+SeedVR2MMRoPE::SeedVR2MMRoPE(const seedvr2::AwaRuntimeSpec& spec) : SeedVR2AwaLayerBase("SeedVR2MMRoPE", true, spec)
+{
+}
+
+int SeedVR2MMRoPE::forward(const std::vector<Mat>& bottom_blobs, std::vector<Mat>& top_blobs,
+                           const Option& opt) const
+{
+    if (require_uploaded() != 0 || bottom_blobs.size() != 1)
+        return -1;
+    const Mat& in = bottom_blobs[0];
+    top_blobs.resize(1);
+    if (top_blobs[0].create(in.w, in.h, in.c, 4, opt.blob_allocator) != AWA_OK)
+        return AWA_ERR_ALLOC;
+    const awa_blob a = in.blob();
+    const awa_blob b = top_blobs[0].blob();
+    const int rc = awa_mmrope(plan_, &a, &b, opt.stream);
+    report(type.c_str(), rc);
+    return rc;
+}
+
+SeedVR2WindowAttention::SeedVR2WindowAttention() : SeedVR2AwaLayerBase("SeedVR2WindowAttention", false)
+{
+}
+
+SeedVR2WindowAttention::SeedVR2WindowAttention(const seedvr2::AwaRuntimeSpec& spec)
+    : SeedVR2AwaLayerBase("SeedVR2WindowAttention", false, spec)
+{
+}
+
+int SeedVR2WindowAttention::forward(const std::vector<Mat>& bottom_blobs, std::vector<Mat>& top_blobs,
+                                    const Option& opt) const
+{
+    if (require_uploaded() != 0 || bottom_blobs.size() != 1)
+        return -1;
+    const Mat& in = bottom_blobs[0];
+    if (in.dims != 3 || in.h % 3 != 0)
+        return -1;
+    top_blobs.resize(1);
+    if (top_blobs[0].create(in.w, in.h / 3, in.c, 4, opt.blob_allocator) != AWA_OK)
+        return AWA_ERR_ALLOC;
+    const awa_blob a = in.blob();
+    const awa_blob b = top_blobs[0].blob();
+    const int rc = awa_window_attention(plan_, &a, &b, opt.use_bf16_storage ? AWA_COMPUTE_BF16 : AWA_COMPUTE_F32,
+                                        opt.stream);
+    report(type.c_str(), rc);
+    return rc;
+}
+
+SeedVR2AWAUnpack::SeedVR2AWAUnpack() : SeedVR2AwaLayerBase("SeedVR2AWAUnpack", false)
+{
+}
+
+SeedVR2AWAUnpack::SeedVR2AWAUnpack(const seedvr2::AwaRuntimeSpec& spec)
+    : SeedVR2AwaLayerBase("SeedVR2AWAUnpack", false, spec)
+{
+}
+
+namespace
+{
+
+// Video and text outputs of Unpack (src/awa/awa_layers.cpp:638-689, :743-846).
+int create_unpack_outputs(const awa_plan_info& info, int heads, int head_dim, const Option& opt,
+                          std::vector<Mat>& top_blobs)
+{
+    const size_t elemsize = opt.use_bf16_storage ? 2 : 4;
+    top_blobs.resize(2);
+    int rc = opt.use_batch_video_layout
+                 ? top_blobs[0].create_4d(head_dim, heads, info.source_w, info.source_h, elemsize, opt.blob_allocator,
+                                          info.source_t)
+                 : top_blobs[0].create(head_dim, heads, info.source_tokens, elemsize, opt.blob_allocator);
+    if (rc == AWA_OK)
+        rc = top_blobs[1].create(head_dim, heads, info.text_tokens, elemsize, opt.blob_allocator);
+    return rc;
+}
+
+} // namespace
+
+int SeedVR2AWAUnpack::forward(const std::vector<Mat>& bottom_blobs, std::vector<Mat>& top_blobs,
+                              const Option& opt) const
+{
+    if (require_uploaded() != 0 || bottom_blobs.size() != 1)
+        return -1;
+    const Mat& in = bottom_blobs[0];
+    if (in.dims != 3)
+        return -1;
+    if (create_unpack_outputs(info_, in.h, in.w, opt, top_blobs) != AWA_OK)
+        return AWA_ERR_ALLOC;
+    const awa_blob a = in.blob();
+    const awa_blob v = top_blobs[0].blob();
+    const awa_blob t = top_blobs[1].blob();
+    const int rc = awa_unpack(plan_, &a, &v, &t, opt.stream);
+    report(type.c_str(), rc);
+    return rc;
+}
+
+int seedvr2_awa_forward_chain(const SeedVR2AWAPack& pack, const SeedVR2AWAUnpack& unpack,
+                              const std::vector<Mat>& bottom_blobs, std::vector<Mat>& top_blobs, const Option& opt)
+{
+    const awa_plan* p = pack.plan();
+    const awa_plan* u = unpack.plan();
+    if (!p || !u || bottom_blobs.size() != 2)
+        return -1;
+    awa_plan_info pi{}, ui{};
+    awa_plan_info_get(p, &pi);
+    awa_plan_info_get(u, &ui);
+    if (pi.source_t != ui.source_t || pi.source_h != ui.source_h || pi.source_w != ui.source_w ||
+        pi.window_count != ui.window_count || pi.sequence_tokens != ui.sequence_tokens || pi.shifted != ui.shifted ||
+        pi.text_tokens != ui.text_tokens)
+        return -1;
+    const awa_blob video = bottom_blobs[0].blob();
+    const awa_blob text = bottom_blobs[1].blob();
+    int heads = 0, head_dim = 0;
+    int rc = awa_qkv_shape(&video, pi.source_tokens, &heads, &head_dim);
+    if (rc != AWA_OK)
+        return rc;
+    if (create_unpack_outputs(pi, heads, head_dim, opt, top_blobs) != AWA_OK)
+        return AWA_ERR_ALLOC;
+    const awa_blob v = top_blobs[0].blob();
+    const awa_blob t = top_blobs[1].blob();
+    rc = awa_forward(p, &video, &text, &v, &t, opt.use_bf16_storage ? AWA_COMPUTE_BF16 : AWA_COMPUTE_F32, opt.stream);
+    report("SeedVR2AWA fused chain", rc);
+    return rc;
+}
+
+namespace
+{
+
+template <class T>
+seedvr2::hip::Layer* create_layer(void* userdata)
+{
+    const auto* spec = static_cast<const seedvr2::AwaRuntimeSpec*>(userdata);
+    return spec ? new T(*spec) : new T();
+}
+
+} // namespace
+
+void register_seedvr2_awa_layers(seedvr2::hip::Net& net)
+{
+    register_seedvr2_awa_layers(net, nullptr);
+}
+
+void register_seedvr2_awa_layers(seedvr2::hip::Net& net, const seedvr2::AwaRuntimeSpec* runtime_spec)
+{
+    void* userdata = const_cast<seedvr2::AwaRuntimeSpec*>(runtime_spec);
+    net.register_custom_layer("SeedVR2AWAPack", create_layer<SeedVR2AWAPack>, nullptr, userdata);
+    net.register_custom_layer("SeedVR2AWAUnpack", create_layer<SeedVR2AWAUnpack>, nullptr, userdata);
+    net.register_custom_layer("SeedVR2MMRoPE", create_layer<SeedVR2MMRoPE>, nullptr, userdata);
+    net.register_custom_layer("SeedVR2WindowAttention", create_layer<SeedVR2WindowAttention>, nullptr, userdata);
+}

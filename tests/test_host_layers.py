@@ -1,0 +1,69 @@
+"""The C++ layer surface (SeedVR2AWAPack / SeedVR2MMRoPE /
+SeedVR2WindowAttention / SeedVR2AWAUnpack over the C ABI), driven by
+tests/cpp/awa_layers_check the way a host of the reference's ncnn layers
+drives them (src/awa/awa_layers.h:47-223)."""
+
+from __future__ import annotations
+
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle as O
+from awa_cases import rel_err
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CHECK = os.path.join(ROOT, "tests", "cpp", "awa_layers_check")
+
+
+def run_check(*args: str) -> subprocess.CompletedProcess:
+    if not os.path.exists(CHECK):
+        pytest.fail(f"{CHECK} missing: build it with `make -C tests/cpp` (part of __graft_entry__.build())")
+    return subprocess.run([CHECK, *args], capture_output=True, text=True, timeout=300)
+
+
+def test_layer_params_and_registration():
+    r = run_check("params")
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "params: all passed" in r.stdout
+
+
+FORWARD_CASES = [
+    # t, h, w, nt, nh, nw, text, shifted, heads, bf16
+    ((1, 16, 16, 1, 8, 8, 64, 0), 4, 0),
+    ((2, 16, 16, 1, 8, 8, 64, 1), 3, 1),
+    ((3, 11, 13, 2, 3, 3, 5, 1), 2, 0),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("params,heads,bf16", FORWARD_CASES)
+def test_layer_chain_matches_oracle(gpu, tmp_path, params, heads, bf16):
+    print(f"layer chain case {params} heads={heads} bf16={bf16}", flush=True)
+    r = run_check("forward", str(tmp_path), *map(str, params), str(heads), str(bf16))
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0, r.stdout + r.stderr
+    t, h, w, nt, nh, nw, text, shifted = params
+    g = O.Geometry(t, h, w, nt, nh, nw, text, bool(shifted))
+    n, d = g.source_tokens, 128
+
+    def load(name, shape):
+        return np.fromfile(os.path.join(tmp_path, name), np.float32).reshape(shape)
+
+    video = load("video_qkv.f32", (n, 3, heads, d))
+    txt = load("text_qkv.f32", (text, 3, heads, d))
+    ref_v, ref_t = O.awa_layer(g, video, txt, heads, d)
+    cu = load("cu_seqlens.f32", (-1,))
+    assert np.array_equal(cu, O.build_maps(g).cu_seqlens.astype(np.float32))
+    for kind in ("staged", "fused"):
+        v = load(f"{kind}_video.f32", (n, heads, d))
+        tt = load(f"{kind}_text.f32", (text, heads, d))
+        if bf16:
+            assert rel_err(v, ref_v) <= 2e-2 and rel_err(tt, ref_t) <= 2e-2, kind
+        else:
+            assert np.max(np.abs(v - ref_v)) <= 1e-4 and np.max(np.abs(tt - ref_t)) <= 1e-4, kind
+    diff = float(r.stdout.strip().split()[-1])
+    assert diff <= (1e-6 if not bf16 else 1e-2)
