@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
@@ -44,6 +45,16 @@ int fail_hip(hipError_t e, const char* what)
 hipStream_t as_stream(void* s)
 {
     return static_cast<hipStream_t>(s);
+}
+
+// Shape trace of the layer blobs when SEEDVR2_TRACE_OPS is set, in the
+// reference's line format (trace_awa_type, src/awa/awa_layers.cpp:189-201).
+void trace_blob(const char* op, const awa_blob* b)
+{
+    static const bool enabled = std::getenv("SEEDVR2_TRACE_OPS") != nullptr;
+    if (enabled && b)
+        std::fprintf(stderr, "awa-trace op=%s dims=%d w=%d h=%d d=%d c=%d elemsize=%d pack=1\n", op, b->dims, b->w,
+                     b->h, b->d, b->c, b->elemsize);
 }
 
 // ---- descriptor helpers (ncnn Mat semantics, elempack 1) ----
@@ -149,7 +160,7 @@ int check_plan_uploaded(const awa_plan* plan)
 }
 
 // Work list of the attention kernel for `heads` heads: every (window, head)
-// unit is split into query blocks of 128 rows; units are placed on the 8
+// unit is split into query blocks of kQueryRows rows; units are placed on the 8
 // XCDs by longest-processing-time first, and each XCD's items are laid out
 // at blockIdx = xcd + 8*j, since workgroups are dispatched round-robin over
 // the XCDs. All query blocks of one unit therefore share one XCD's L2 for
@@ -594,6 +605,10 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
         return fail(AWA_ERR_INVALID, "null blob");
     if (compute != AWA_COMPUTE_F32 && compute != AWA_COMPUTE_BF16)
         return fail(AWA_ERR_INVALID, "unknown compute mode");
+    trace_blob("forward.video.in", video_qkv);
+    trace_blob("forward.text.in", text_qkv);
+    trace_blob("forward.video.out", video_out);
+    trace_blob("forward.text.out", text_out);
     QkvLayout vl, tl;
     if (!describe_qkv(*video_qkv, plan->source_tokens, vl) || !describe_qkv(*text_qkv, plan->text_tokens, tl) ||
         vl.heads != tl.heads || vl.head_dim != tl.head_dim || video_qkv->elemsize != text_qkv->elemsize)
@@ -679,6 +694,9 @@ int awa_pack(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* te
         return rc;
     if (!video_qkv || !text_qkv || !packed || !cu_seqlens)
         return fail(AWA_ERR_INVALID, "null blob");
+    trace_blob("pack.video.in", video_qkv);
+    trace_blob("pack.text.in", text_qkv);
+    trace_blob("pack.out", packed);
     QkvLayout vl, tl;
     if (!describe_qkv(*video_qkv, plan->source_tokens, vl) || !describe_qkv(*text_qkv, plan->text_tokens, tl) ||
         vl.heads != tl.heads || vl.head_dim != tl.head_dim)
@@ -706,6 +724,7 @@ int awa_mmrope(const awa_plan* plan, const awa_blob* input, const awa_blob* outp
         return rc;
     if (!input || !output)
         return fail(AWA_ERR_INVALID, "null blob");
+    trace_blob("rope.in", input);
     // src/awa/awa_layers.cpp:997-1004: w >= rope_dim, h % 3 == 0, c == S.
     if (!input->data || input->dims != 3 || input->w < plan->rope_dim || input->h <= 0 || input->h % 3 != 0 ||
         input->c != plan->sequence_tokens || (input->elemsize != 2 && input->elemsize != 4))
@@ -730,6 +749,7 @@ int awa_window_attention(const awa_plan* plan, const awa_blob* input, const awa_
         return fail(AWA_ERR_INVALID, "null blob");
     if (compute != AWA_COMPUTE_F32 && compute != AWA_COMPUTE_BF16)
         return fail(AWA_ERR_INVALID, "unknown compute mode");
+    trace_blob("attention.in", input);
     if (!input->data || input->dims != 3 || input->w <= 0 || input->h <= 0 || input->h % 3 != 0 ||
         input->c != plan->sequence_tokens || (input->elemsize != 2 && input->elemsize != 4))
         return fail(AWA_ERR_INVALID, "invalid WindowAttention input");
@@ -782,6 +802,9 @@ int awa_unpack(const awa_plan* plan, const awa_blob* packed, const awa_blob* vid
         return rc;
     if (!packed || !video_out || !text_out)
         return fail(AWA_ERR_INVALID, "null blob");
+    trace_blob("unpack.in", packed);
+    trace_blob("unpack.video.out", video_out);
+    trace_blob("unpack.text.out", text_out);
     // src/awa/awa_layers.cpp:755-762
     if (!packed->data || packed->dims != 3 || packed->w <= 0 || packed->h <= 0 ||
         packed->c != plan->sequence_tokens || (packed->elemsize != 2 && packed->elemsize != 4))

@@ -67,3 +67,18 @@ def test_layer_chain_matches_oracle(gpu, tmp_path, params, heads, bf16):
             assert np.max(np.abs(v - ref_v)) <= 1e-4 and np.max(np.abs(tt - ref_t)) <= 1e-4, kind
     diff = float(r.stdout.strip().split()[-1])
     assert diff <= (1e-6 if not bf16 else 1e-2)
+
+
+@pytest.mark.gpu
+def test_shape_trace(gpu, tmp_path):
+    """SEEDVR2_TRACE_OPS prints one line per layer blob, in the reference's format."""
+    env = dict(os.environ, SEEDVR2_TRACE_OPS="1")
+    r = subprocess.run([CHECK, "forward", str(tmp_path), "1", "16", "16", "1", "8", "8", "64", "0", "2", "0"],
+                       capture_output=True, text=True, timeout=300, env=env)
+    assert r.returncode == 0, r.stderr
+    lines = [l for l in r.stderr.splitlines() if l.startswith("awa-trace op=")]
+    ops = [l.split()[1][3:] for l in lines]
+    for op in ("pack.video.in", "pack.text.in", "pack.out", "rope.in", "attention.in", "unpack.in",
+               "unpack.video.out", "unpack.text.out", "forward.video.in"):
+        assert op in ops, op
+    assert "awa-trace op=pack.video.in dims=3 w=128 h=6 d=1 c=256 elemsize=4 pack=1" in lines
