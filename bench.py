@@ -12,10 +12,12 @@ including the fp32 -> bf16 conversion at block 9.
 
 Prints one JSON line: the step's window-attention throughput (TFLOP/s over
 the algorithmic FLOPs sum_w 4 L_w^2 d H), ms per step, the bf16 layers' share
-of bf16 MFMA peak, the roofline entry of the dominant kernel (the fp32
-attention kernel, timed with HIP events on its own stream) and the CPU
-baseline (the oracle's single-threaded restatement of the reference's CPU
-layer, on a bounded sample).
+of bf16 MFMA peak, the roofline entry of the dominant attention kernel (the
+fp32 or bf16 instance with the larger share of the step, timed with HIP
+events on the stack's stream; HBM-bound when its arithmetic intensity is
+below the ridge point, MFMA-bound otherwise) and the CPU baseline (the
+oracle's single-threaded restatement of the reference's CPU layer, on a
+bounded sample).
 """
 
 from __future__ import annotations
@@ -168,8 +170,20 @@ def main() -> int:
     dom_name = "window_attention_kernel<f32 MFMA>" if fp32_total >= bf16_total else "window_attention_kernel<bf16 MFMA>"
     avg_flops = float(flops[dom].mean())
     avg_ms = float(att[dom].mean())
-    achieved = avg_flops / (avg_ms * 1e-3) / 1e12
-    peak = (PEAK_FP32 if fp32_total >= bf16_total else PEAK_BF16) / 1e12
+    # Roofline of the dominant kernel: algorithmic bytes per launch are the QKV
+    # rows read once and the outputs written once, (N + T_x) * H * d * (3 s_in + s_out).
+    elem = 4 if dom is fp32_idx else 2
+    alg_bytes = float((N + TEXT) * HEADS * HEAD_DIM * 4 * elem)
+    mfma_peak = PEAK_FP32 if dom is fp32_idx else PEAK_BF16
+    intensity = avg_flops / alg_bytes
+    if intensity < mfma_peak / PEAK_HBM:
+        bound, unit = "hbm", "GB/s"
+        achieved = alg_bytes / (avg_ms * 1e-3) / 1e9
+        peak = PEAK_HBM / 1e9
+    else:
+        bound, unit = "mfma", "TFLOP/s"
+        achieved = avg_flops / (avg_ms * 1e-3) / 1e12
+        peak = mfma_peak / 1e12
     traffic = None
     if args.traffic_json and os.path.exists(args.traffic_json):
         with open(args.traffic_json) as f:
@@ -215,13 +229,17 @@ def main() -> int:
                         for k, v in fp32_layers.items()},
         "roofline": {
             "kernel": dom_name,
-            "bound": "mfma",
+            "bound": bound,
             "achieved": round(achieved, 2),
             "peak": round(peak, 1),
-            "unit": "TFLOP/s",
+            "unit": unit,
             "frac": round(achieved / peak, 4),
             "traffic": traffic,
             "flops_per_launch": avg_flops,
+            "algorithmic_bytes_per_launch": alg_bytes,
+            "arithmetic_intensity": round(intensity, 1),
+            "tflops": round(avg_flops / (avg_ms * 1e-3) / 1e12, 2),
+            "frac_of_mfma_peak": round(avg_flops / (avg_ms * 1e-3) / mfma_peak, 4),
             "avg_launch_ms": round(avg_ms, 5),
         },
     }
