@@ -30,6 +30,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "awa_kernels.h"
 
@@ -281,21 +282,42 @@ __device__ __forceinline__ void store_row(TOut* dst, const f32x16 (&o)[4], float
                    o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
 }
 
+// max / sum of x over lanes l and l ^ 32 (v_permlane32_swap hands each lane
+// its partner's value in one of the two results, its own in the other).
+__device__ __forceinline__ float max_xor32(float x)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float sum_xor32(float x)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <int N>
+using Buf = std::integral_constant<int, N>;
+
 template <typename TIn, typename TOut, bool BF16, bool FUSED>
 __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const AttentionLaunch p)
 {
     // Key tile and LDS layout (pitches in elements; rows stay 16-byte aligned).
-    // 64-key tiles (two 32-key score blocks) on bf16 MFMA, 32 on fp32 MFMA.
+    // 64-key tiles (two 32-key score blocks) on bf16 MFMA, 32 on fp32 MFMA;
+    // two buffers, so that tile t+1 is staged while tile t is computed.
     constexpr int KT = BF16 ? 64 : 32;
     constexpr int kKPitch = BF16 ? kHeadDim + 8 : kHeadDim + 4;
     constexpr int kVPitch = BF16 ? KT + 8 : KT + 4;
     constexpr int kElem = BF16 ? 2 : 4;
     constexpr int kRW = kRawWords8<TIn>;
+    constexpr int kKBytes = KT * kKPitch * kElem;
+    constexpr int kVBytes = kHeadDim * kVPitch * kElem;
+    constexpr int kBlocks = KT / 32; // 32-key score blocks per tile
 
-    __shared__ __attribute__((aligned(16))) unsigned char k_lds[KT * kKPitch * kElem];
-    __shared__ __attribute__((aligned(16))) unsigned char v_lds[kHeadDim * kVPitch * kElem];
+    __shared__ __attribute__((aligned(16))) unsigned char k_lds[2 * kKBytes];
+    __shared__ __attribute__((aligned(16))) unsigned char v_lds[2 * kVBytes];
     __shared__ __attribute__((aligned(16))) float rope_lds[FUSED ? kMaxRopeCoords * kRopeRow : 4];
-    extern __shared__ __attribute__((aligned(16))) unsigned char row_dyn[]; // fused: row table
+    extern __shared__ __attribute__((aligned(16))) unsigned char row_dyn[]; // row table
 
     const WorkItem item = p.work[blockIdx.x];
     if (item.window < 0)
@@ -310,6 +332,8 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
     const int col = lane & 31;
     const int half = lane >> 5;
     const int head_off = head * kHeadDim;
+    const int tiles = (L + KT - 1) / KT;
+    const int table_rows = (p.max_window_tokens + 63) & ~63;
 
     // Wave-uniform scalars read once from the kernel arguments (plain values,
     // so that per-lane selects never turn into indexed struct accesses).
@@ -319,13 +343,28 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
     const long long v_qkv = p.video.qkv_stride;
     const long long t_tok = p.text.token_stride;
     const long long t_qkv = p.text.qkv_stride;
-    const TIn* packed_base = static_cast<const TIn*>(p.packed_in);
+    const TIn* const packed_base = static_cast<const TIn*>(p.packed_in);
     const long long packed_row = p.packed_in_row;
     const long long packed_qkv = static_cast<long long>(p.heads) * kHeadDim;
     const float scale_log2 = p.scale_log2;
 
-    // RoPE table: the loads are issued first and land in LDS after the
-    // Q and first-tile loads below are in flight.
+    // Element pointer of (window row i < L, qkv, head) in its source blob.
+    auto row_ptr = [&](int i, int qkv) -> const TIn* {
+        if constexpr (FUSED)
+        {
+            const RowRef r =
+                decode_row(encode_row(win, i), win.t0, win.h0, win.w0, p.text_tokens, p.source_h, p.source_w);
+            return r.text ? text_base + r.k * t_tok + qkv * t_qkv + head_off
+                          : video_base + static_cast<long long>(r.token) * v_tok + qkv * v_qkv + head_off;
+        }
+        else
+        {
+            return packed_base + (win.seq_start + i) * packed_row + qkv * packed_qkv + head_off;
+        }
+    };
+
+    // RoPE table: its loads are issued first and land in LDS after the Q
+    // and first-tile loads are in flight.
     constexpr int kRopePerThread = (kMaxRopeCoords * kRopeRow + kThreads - 1) / kThreads;
     float rope_reg[FUSED ? kRopePerThread : 1];
     if constexpr (FUSED)
@@ -339,41 +378,48 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
         }
     }
 
-    // Row table (fused mode, LDS): for every window row the element offset of
-    // (row, qkv 0, head 0) in its blob, bit 63 marking text rows, and its RoPE
-    // coordinates packed as ct | ch << 8 | cw << 16 (all below 128).
-    unsigned long long* row_off = reinterpret_cast<unsigned long long*>(row_dyn);
-    uint32_t* row_code = reinterpret_cast<uint32_t*>(row_off + p.max_window_tokens);
-
-    // Pointer to (row i, qkv, head). Rows past the window end are clamped to
-    // its last row: their keys are masked and their values weighted by zero,
-    // so every load is in bounds and unconditional.
-    auto row_src = [&](int i, int qkv) -> const TIn* {
-        i = min(i, L - 1);
-        if constexpr (FUSED)
-        {
-            const unsigned long long off = row_off[i];
-            const long long e = static_cast<long long>(off & 0x7fffffffffffffffull);
-            const TIn* vb = video_base + qkv * v_qkv;
-            const TIn* tb = text_base + qkv * t_qkv;
-            return ((off >> 63) ? tb : vb) + e + head_off;
-        }
-        else
-        {
-            return packed_base + (win.seq_start + i) * packed_row + qkv * packed_qkv + head_off;
-        }
-    };
-    auto row_coords = [&](int i, int& ct, int& ch, int& cw) {
-        const uint32_t code = row_code[min(i, L - 1)];
-        ct = static_cast<int>(code & 255u);
-        ch = static_cast<int>((code >> 8) & 255u);
-        cw = static_cast<int>((code >> 16) & 255u);
-    };
-
     const int wave_row0 = qblock * kQueryRows + wave * 32;
     const bool wave_active = wave_row0 < L;
     const int qi = wave_row0 + col;
     const bool q_valid = qi < L;
+    const int q_row = min(qi, L - 1);
+
+    // Q rows go straight to registers; their addresses do not need the table.
+    uint32_t qraw[8 * kRW];
+    {
+        const TIn* q_src = row_ptr(q_row, 0);
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+            load_raw8(q_src + (BF16 ? 16 * c + 8 * half : 64 * half + 8 * c), qraw + c * kRW);
+    }
+
+    // Row table (LDS), padded to whole tiles with copies of the last row so
+    // that every staging load is unconditional and in bounds (padded keys are
+    // masked, padded values weighted by zero): the byte offsets of each row's
+    // K and V from a kernel-argument base pointer (so that the loads stay
+    // global-memory loads, which the LDS counters do not wait on) and, in
+    // fused mode, its RoPE coordinates ct | ch << 8 | cw << 16 (all below 128)
+    // with byte 3 naming the table's identity row.
+    const unsigned char* const load_base =
+        reinterpret_cast<const unsigned char*>(FUSED ? static_cast<const void*>(video_base)
+                                                     : static_cast<const void*>(packed_base));
+    long long* row_k = reinterpret_cast<long long*>(row_dyn);
+    long long* row_v = row_k + table_rows;
+    uint32_t* row_code = reinterpret_cast<uint32_t*>(row_v + table_rows);
+    for (int i = tid; i < tiles * KT; i += kThreads)
+    {
+        const int src = min(i, L - 1);
+        row_k[i] = reinterpret_cast<const unsigned char*>(row_ptr(src, 1)) - load_base;
+        row_v[i] = reinterpret_cast<const unsigned char*>(row_ptr(src, 2)) - load_base;
+        if constexpr (FUSED)
+        {
+            const RowRef r =
+                decode_row(encode_row(win, src), win.t0, win.h0, win.w0, p.text_tokens, p.source_h, p.source_w);
+            row_code[i] = static_cast<uint32_t>(r.ct) | (static_cast<uint32_t>(r.ch) << 8) |
+                          (static_cast<uint32_t>(r.cw) << 16) | (static_cast<uint32_t>(p.rope_coords) << 24);
+        }
+    }
+    __syncthreads();
 
     // ---- staging assignment ----
     // Loads are coalesced: 16 consecutive threads read the 16 chunks of 8
@@ -400,8 +446,8 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
         rope_col[q] = axis < 3 ? 2 * (pair - axis * kRopePairs) : 0;
     }
 
-    // Two register stages: the loads of tile t+2 are issued while tile t is
-    // computed, so two tiles' loads are always in flight.
+    // Two register stages: tile t+1 is written to LDS during step t and its
+    // registers then take the loads of tile t+3.
     struct Stage
     {
         uint32_t k[kKRows * kRW];
@@ -412,13 +458,18 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
     auto load_tile = [&](int tile, Stage& st) {
 #pragma unroll
         for (int j = 0; j < kKRows; j++)
-            load_raw8(row_src(tile * KT + kr0 + 32 * j, 1) + 8 * kc, st.k + j * kRW);
+            load_raw8(reinterpret_cast<const TIn*>(load_base + row_k[tile * KT + kr0 + 32 * j]) + 8 * kc,
+                      st.k + j * kRW);
 #pragma unroll
         for (int j = 0; j < kVKeys; j++)
-            load_raw8(row_src(tile * KT + kVKeys * kr0 + j, 2) + 8 * kc, st.v + j * kRW);
+            load_raw8(reinterpret_cast<const TIn*>(load_base + row_v[tile * KT + kVKeys * kr0 + j]) + 8 * kc,
+                      st.v + j * kRW);
     };
 
-    auto store_tile = [&](int tile, const Stage& st) {
+    auto store_tile = [&](int tile, const Stage& st, auto buf_c) {
+        constexpr int buf = decltype(buf_c)::value;
+        unsigned char* const kb = k_lds + buf * kKBytes;
+        unsigned char* const vb = v_lds + buf * kVBytes;
 #pragma unroll
         for (int j = 0; j < kKRows; j++)
         {
@@ -427,7 +478,7 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
             raw_to_float8<TIn>(st.k + j * kRW, kv);
             if constexpr (FUSED)
             {
-                const uint32_t code = row_code[min(tile * KT + row, L - 1)];
+                const uint32_t code = row_code[tile * KT + row];
 #pragma unroll
                 for (int q = 0; q < 4; q++)
                 {
@@ -441,13 +492,13 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
             }
             if constexpr (BF16)
             {
-                uint16_t* ks = reinterpret_cast<uint16_t*>(k_lds) + row * kKPitch + 8 * kc;
+                uint16_t* ks = reinterpret_cast<uint16_t*>(kb) + row * kKPitch + 8 * kc;
                 *reinterpret_cast<uint4*>(ks) = make_uint4(cvt_pk_bf16(kv[0], kv[1]), cvt_pk_bf16(kv[2], kv[3]),
                                                            cvt_pk_bf16(kv[4], kv[5]), cvt_pk_bf16(kv[6], kv[7]));
             }
             else
             {
-                float* ks = reinterpret_cast<float*>(k_lds) + row * kKPitch + 8 * kc;
+                float* ks = reinterpret_cast<float*>(kb) + row * kKPitch + 8 * kc;
                 *reinterpret_cast<float4*>(ks) = make_float4(kv[0], kv[1], kv[2], kv[3]);
                 *reinterpret_cast<float4*>(ks + 4) = make_float4(kv[4], kv[5], kv[6], kv[7]);
             }
@@ -467,7 +518,7 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
                     word = __builtin_amdgcn_perm(b[e >> 1], a[e >> 1], (e & 1) ? 0x07060302u : 0x05040100u);
                 else
                     word = cvt_pk_bf16(__uint_as_float(a[e]), __uint_as_float(b[e]));
-                *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(v_lds) + (8 * kc + e) * kVPitch + key) = word;
+                *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(vb) + (8 * kc + e) * kVPitch + key) = word;
             }
             else
             {
@@ -476,35 +527,14 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
                     v = (e & 1) ? bf16_hi(st.v[e >> 1]) : bf16_lo(st.v[e >> 1]);
                 else
                     v = __uint_as_float(st.v[e]);
-                reinterpret_cast<float*>(v_lds)[(8 * kc + e) * kVPitch + key] = v;
+                reinterpret_cast<float*>(vb)[(8 * kc + e) * kVPitch + key] = v;
             }
         }
     };
 
-    const int tiles = (L + KT - 1) / KT;
-
-    // ---- prologue: row table (ALU only) while the RoPE table's loads are in
-    // flight; then Q and the first two tiles' loads; then the RoPE table
-    // reaches LDS ----
-    if constexpr (FUSED)
-    {
-        for (int i = tid; i < L; i += kThreads)
-        {
-            const RowRef r =
-                decode_row(encode_row(win, i), win.t0, win.h0, win.w0, p.text_tokens, p.source_h, p.source_w);
-            row_off[i] = r.text ? (0x8000000000000000ull | static_cast<unsigned long long>(r.k * t_tok))
-                                : static_cast<unsigned long long>(static_cast<long long>(r.token) * v_tok);
-            // Byte 3 names the identity row of the RoPE table (unrotated pairs).
-            row_code[i] = static_cast<uint32_t>(r.ct) | (static_cast<uint32_t>(r.ch) << 8) |
-                          (static_cast<uint32_t>(r.cw) << 16) | (static_cast<uint32_t>(p.rope_coords) << 24);
-        }
-        __syncthreads();
-    }
-    const TIn* q_src = row_src(qi, 0);
-    uint32_t qraw[8 * kRW];
-#pragma unroll
-    for (int c = 0; c < 8; c++)
-        load_raw8(q_src + (BF16 ? 16 * c + 8 * half : 64 * half + 8 * c), qraw + c * kRW);
+    // ---- prologue: first two tiles' loads, the RoPE table into LDS (plus an
+    // identity row after the last coordinate), Q rotated and scaled in
+    // registers, tile 0 staged ----
     load_tile(0, st0);
     // With fp32 inputs the raw Q registers are twice as large; the second
     // tile then follows once Q has been converted.
@@ -514,7 +544,10 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
     int q_ct = 0, q_ch = 0, q_cw = 0;
     if constexpr (FUSED)
     {
-        row_coords(qi, q_ct, q_ch, q_cw);
+        const uint32_t code = row_code[q_row];
+        q_ct = static_cast<int>(code & 255u);
+        q_ch = static_cast<int>((code >> 8) & 255u);
+        q_cw = static_cast<int>((code >> 16) & 255u);
         const int n = p.rope_coords * kRopeRow;
 #pragma unroll
         for (int j = 0; j < kRopePerThread; j++)
@@ -523,54 +556,54 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
             if (e < n)
                 rope_lds[e] = rope_reg[j];
         }
-        // Identity row after the last coordinate: (cos, sin) = (1, 0).
         if (tid < kRopeRow)
             rope_lds[n + tid] = (tid & 1) ? 0.f : 1.f;
         __syncthreads();
     }
 
-    // ---- Q into registers (B operand of S^T = K Q^T), scaled by log2(e)/sqrt(d) ----
+    // Q into registers (B operand of S^T = K Q^T), scaled by log2(e)/sqrt(d).
     // bf16: lane holds features 16c + 8*half + [0,8) for c = 0..7.
     // fp32: lane holds features 64*half + [0,64).
     bf16x8 qb[BF16 ? 8 : 1];
     float qf[BF16 ? 1 : 64];
-    {
-        const int ct = q_ct, ch = q_ch, cw = q_cw;
 #pragma unroll
-        for (int c = 0; c < 8; c++)
+    for (int c = 0; c < 8; c++)
+    {
+        float v[8];
+        raw_to_float8<TIn>(qraw + c * kRW, v);
+        if constexpr (FUSED)
         {
-            float v[8];
-            raw_to_float8<TIn>(qraw + c * kRW, v);
-            if constexpr (FUSED)
-            {
-                // 4 pairs from pair 8c + 4*half (bf16) or 32*half + 4c (fp32).
-                if constexpr (BF16)
-                    rope_slice<4>(v, 2 * c + half, ct, ch, cw, rope_lds);
-                else
-                    rope_slice<4>(v, 8 * half + c, ct, ch, cw, rope_lds);
-            }
+            // 4 pairs from pair 8c + 4*half (bf16) or 32*half + 4c (fp32).
+            if constexpr (BF16)
+                rope_slice<4>(v, 2 * c + half, q_ct, q_ch, q_cw, rope_lds);
+            else
+                rope_slice<4>(v, 8 * half + c, q_ct, q_ch, q_cw, rope_lds);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            v[e] *= scale_log2;
+        if constexpr (BF16)
+        {
+            bf16x8 x;
 #pragma unroll
             for (int e = 0; e < 8; e++)
-                v[e] *= scale_log2;
-            if constexpr (BF16)
-            {
-                bf16x8 x;
+                x[e] = static_cast<__bf16>(v[e]);
+            qb[c] = x;
+        }
+        else
+        {
 #pragma unroll
-                for (int e = 0; e < 8; e++)
-                    x[e] = static_cast<__bf16>(v[e]);
-                qb[c] = x;
-            }
-            else
-            {
-#pragma unroll
-                for (int e = 0; e < 8; e++)
-                    qf[8 * c + e] = v[e];
-            }
+            for (int e = 0; e < 8; e++)
+                qf[8 * c + e] = v[e];
         }
     }
 
     if (!kEarlySecondTile && tiles > 1)
         load_tile(1, st1);
+    store_tile(0, st0, Buf<0>{});
+    if (tiles > 2)
+        load_tile(2, st0);
+    __syncthreads();
 
     f32x16 o[4];
 #pragma unroll
@@ -582,160 +615,170 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
     float row_sum = 0.f;       // partial sum over this lane's keys
 
     const int krow = key_permute(col);
-    auto compute_tile = [&](int tile) {
-        if (wave_active)
+
+    // S^T = K Q^T of one tile: one 32x32 block per 32 keys; chains interleaved.
+    auto scores = [&](f32x16 (&s)[kBlocks], auto buf_c) {
+        constexpr int buf = decltype(buf_c)::value;
+#pragma unroll
+        for (int b = 0; b < kBlocks; b++)
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                s[b][i] = 0.f;
+        if constexpr (BF16)
         {
-            constexpr int kBlocks = KT / 32; // 32-key blocks in this tile
-            f32x16 s[kBlocks];
+            const uint16_t* ks =
+                reinterpret_cast<const uint16_t*>(k_lds + buf * kKBytes) + krow * kKPitch + 8 * half;
+            bf16x8 ka[kBlocks][8];
 #pragma unroll
-            for (int b = 0; b < kBlocks; b++)
-#pragma unroll
-                for (int i = 0; i < 16; i++)
-                    s[b][i] = 0.f;
-            // ---- S^T = K Q^T: one 32x32 block per 32 keys; chains interleaved ----
-            if constexpr (BF16)
-            {
-                const uint16_t* ks = reinterpret_cast<const uint16_t*>(k_lds) + krow * kKPitch + 8 * half;
-                bf16x8 ka[kBlocks][8];
-#pragma unroll
-                for (int c = 0; c < 8; c++)
-#pragma unroll
-                    for (int b = 0; b < kBlocks; b++)
-                        ka[b][c] = *reinterpret_cast<const bf16x8*>(ks + b * 32 * kKPitch + 16 * c);
-#pragma unroll
-                for (int c = 0; c < 8; c++)
-#pragma unroll
-                    for (int b = 0; b < kBlocks; b++)
-                        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[b][c], qb[c], s[b], 0, 0, 0);
-            }
-            else
-            {
-                // One chain over this lane's 64 features (32x32x2 f32 MFMAs).
-                const float* ks = reinterpret_cast<const float*>(k_lds) + krow * kKPitch + 64 * half;
-#pragma unroll
-                for (int c4 = 0; c4 < 16; c4++)
-                {
-                    const float4 ka = *reinterpret_cast<const float4*>(ks + 4 * c4);
-                    s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.x, qf[4 * c4 + 0], s[0], 0, 0, 0);
-                    s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.y, qf[4 * c4 + 1], s[0], 0, 0, 0);
-                    s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.z, qf[4 * c4 + 2], s[0], 0, 0, 0);
-                    s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.w, qf[4 * c4 + 3], s[0], 0, 0, 0);
-                }
-            }
-
-            // ---- online softmax: register i of block b holds key 32b + 16*(i/8) + 8*half + i%8 ----
-            if (tile == tiles - 1 && (L % KT))
-            {
-                const int key0 = tile * KT + 8 * half;
+            for (int c = 0; c < 8; c++)
 #pragma unroll
                 for (int b = 0; b < kBlocks; b++)
+                    ka[b][c] = *reinterpret_cast<const bf16x8*>(ks + b * 32 * kKPitch + 16 * c);
 #pragma unroll
-                    for (int i = 0; i < 16; i++)
-                        if (key0 + 32 * b + 16 * (i >> 3) + (i & 7) >= L)
-                            s[b][i] = -INFINITY;
-            }
-            float tile_max = s[0][0];
-#pragma unroll
-            for (int b = 0; b < kBlocks; b++)
-#pragma unroll
-                for (int i = 0; i < 16; i++)
-                    tile_max = fmaxf(tile_max, s[b][i]);
-            tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
-            if (__any(tile_max > row_max + kRescaleThreshold))
-            {
-                const float new_max = fmaxf(row_max, tile_max);
-                const float alpha = __builtin_amdgcn_exp2f(row_max - new_max);
-                row_max = new_max;
-                row_sum *= alpha;
-#pragma unroll
-                for (int db = 0; db < 4; db++)
-#pragma unroll
-                    for (int i = 0; i < 16; i++)
-                        o[db][i] *= alpha;
-            }
-            float psum = 0.f;
-#pragma unroll
-            for (int b = 0; b < kBlocks; b++)
-#pragma unroll
-                for (int i = 0; i < 16; i++)
-                {
-                    s[b][i] = __builtin_amdgcn_exp2f(s[b][i] - row_max);
-                    psum += s[b][i];
-                }
-            row_sum += psum;
-
-            // ---- O^T += V^T P^T ----
-            if constexpr (BF16)
-            {
-                bf16x8 pb[2 * kBlocks];
+            for (int c = 0; c < 8; c++)
 #pragma unroll
                 for (int b = 0; b < kBlocks; b++)
+                    s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[b][c], qb[c], s[b], 0, 0, 0);
+        }
+        else
+        {
+            // One chain over this lane's 64 features (32x32x2 f32 MFMAs).
+            const float* ks = reinterpret_cast<const float*>(k_lds + buf * kKBytes) + krow * kKPitch + 64 * half;
 #pragma unroll
-                    for (int e = 0; e < 8; e++)
-                    {
-                        pb[2 * b][e] = static_cast<__bf16>(s[b][e]);
-                        pb[2 * b + 1][e] = static_cast<__bf16>(s[b][8 + e]);
-                    }
-                const uint16_t* vt = reinterpret_cast<const uint16_t*>(v_lds);
-#pragma unroll
-                for (int db = 0; db < 4; db++)
-                {
-                    const int d = db * 32 + col;
-                    const uint16_t* vrow = vt + d * kVPitch;
-                    const int swz = 8 * vt_swizzle<KT>(d >> 3);
-                    bf16x8 va[2 * kBlocks];
-#pragma unroll
-                    for (int j = 0; j < 2 * kBlocks; j++)
-                        va[j] = *reinterpret_cast<const bf16x8*>(vrow + ((8 * half + 16 * j) ^ swz));
-#pragma unroll
-                    for (int j = 0; j < 2 * kBlocks; j++)
-                        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[j], pb[j], o[db], 0, 0, 0);
-                }
-            }
-            else
+            for (int c4 = 0; c4 < 16; c4++)
             {
-                const float* vt = reinterpret_cast<const float*>(v_lds);
+                const float4 ka = *reinterpret_cast<const float4*>(ks + 4 * c4);
+                s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.x, qf[4 * c4 + 0], s[0], 0, 0, 0);
+                s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.y, qf[4 * c4 + 1], s[0], 0, 0, 0);
+                s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.z, qf[4 * c4 + 2], s[0], 0, 0, 0);
+                s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.w, qf[4 * c4 + 3], s[0], 0, 0, 0);
+            }
+        }
+    };
+
+    // Online softmax of one tile's scores, then O^T += V^T P^T.
+    // Register i of score block b holds key 32b + 16*(i/8) + 8*half + i%8.
+    auto softmax_pv = [&](f32x16 (&s)[kBlocks], int tile, auto buf_c) {
+        constexpr int buf = decltype(buf_c)::value;
+        if (tile == tiles - 1 && (L % KT))
+        {
+            const int key0 = tile * KT + 8 * half;
 #pragma unroll
-                for (int db = 0; db < 4; db++)
+            for (int b = 0; b < kBlocks; b++)
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    if (key0 + 32 * b + 16 * (i >> 3) + (i & 7) >= L)
+                        s[b][i] = -INFINITY;
+        }
+        float tile_max = s[0][0];
+#pragma unroll
+        for (int b = 0; b < kBlocks; b++)
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                tile_max = fmaxf(tile_max, s[b][i]);
+        tile_max = max_xor32(tile_max);
+        if (__any(tile_max > row_max + kRescaleThreshold))
+        {
+            const float new_max = fmaxf(row_max, tile_max);
+            const float alpha = __builtin_amdgcn_exp2f(row_max - new_max);
+            row_max = new_max;
+            row_sum *= alpha;
+#pragma unroll
+            for (int db = 0; db < 4; db++)
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    o[db][i] *= alpha;
+        }
+        float psum = 0.f;
+#pragma unroll
+        for (int b = 0; b < kBlocks; b++)
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+            {
+                s[b][i] = __builtin_amdgcn_exp2f(s[b][i] - row_max);
+                psum += s[b][i];
+            }
+        row_sum += psum;
+
+        if constexpr (BF16)
+        {
+            bf16x8 pb[2 * kBlocks];
+#pragma unroll
+            for (int b = 0; b < kBlocks; b++)
+#pragma unroll
+                for (int e = 0; e < 8; e++)
                 {
-                    const int d = db * 32 + col;
-                    const float* vrow = vt + d * kVPitch;
-                    const int swz = 8 * vt_swizzle<KT>(d >> 3);
+                    pb[2 * b][e] = static_cast<__bf16>(s[b][e]);
+                    pb[2 * b + 1][e] = static_cast<__bf16>(s[b][8 + e]);
+                }
+            const uint16_t* vt = reinterpret_cast<const uint16_t*>(v_lds + buf * kVBytes);
 #pragma unroll
-                    for (int g = 0; g < 4; g++)
-                    {
-                        const float4 va =
-                            *reinterpret_cast<const float4*>(vrow + ((16 * (g >> 1) + 8 * half + 4 * (g & 1)) ^ swz));
-                        o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.x, s[0][4 * g + 0], o[db], 0, 0, 0);
-                        o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.y, s[0][4 * g + 1], o[db], 0, 0, 0);
-                        o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.z, s[0][4 * g + 2], o[db], 0, 0, 0);
-                        o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.w, s[0][4 * g + 3], o[db], 0, 0, 0);
-                    }
+            for (int db = 0; db < 4; db++)
+            {
+                const int d = db * 32 + col;
+                const uint16_t* vrow = vt + d * kVPitch;
+                const int swz = 8 * vt_swizzle<KT>(d >> 3);
+                bf16x8 va[2 * kBlocks];
+#pragma unroll
+                for (int j = 0; j < 2 * kBlocks; j++)
+                    va[j] = *reinterpret_cast<const bf16x8*>(vrow + ((8 * half + 16 * j) ^ swz));
+#pragma unroll
+                for (int j = 0; j < 2 * kBlocks; j++)
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[j], pb[j], o[db], 0, 0, 0);
+            }
+        }
+        else
+        {
+            const float* vt = reinterpret_cast<const float*>(v_lds + buf * kVBytes);
+#pragma unroll
+            for (int db = 0; db < 4; db++)
+            {
+                const int d = db * 32 + col;
+                const float* vrow = vt + d * kVPitch;
+                const int swz = 8 * vt_swizzle<KT>(d >> 3);
+#pragma unroll
+                for (int g = 0; g < 4; g++)
+                {
+                    const float4 va =
+                        *reinterpret_cast<const float4*>(vrow + ((16 * (g >> 1) + 8 * half + 4 * (g & 1)) ^ swz));
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.x, s[0][4 * g + 0], o[db], 0, 0, 0);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.y, s[0][4 * g + 1], o[db], 0, 0, 0);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.z, s[0][4 * g + 2], o[db], 0, 0, 0);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.w, s[0][4 * g + 3], o[db], 0, 0, 0);
                 }
             }
         }
     };
 
-    // One key tile: stage it into LDS, then refill its registers with the
-    // tile two steps ahead while the scores and PV products are computed.
-    auto step = [&](int tile, Stage& st) {
-        store_tile(tile, st);
-        __syncthreads();
-        if (tile + 2 < tiles)
-            load_tile(tile + 2, st);
-        compute_tile(tile);
+    // Step t: scores of tile t (LDS buffer t & 1); meanwhile tile t+1 goes
+    // from its registers into the other buffer and the registers take the
+    // loads of tile t+3; then softmax and PV of tile t. One barrier per step:
+    // it publishes tile t+1 and retires every read of buffer t & 1.
+    auto step = [&](int tile, Stage& next, auto buf_c) {
+        constexpr int buf = decltype(buf_c)::value;
+        f32x16 s[kBlocks];
+        if (wave_active)
+            scores(s, buf_c);
+        if (tile + 1 < tiles)
+        {
+            store_tile(tile + 1, next, Buf<buf ^ 1>{});
+            if (tile + 3 < tiles)
+                load_tile(tile + 3, next);
+        }
+        if (wave_active)
+            softmax_pv(s, tile, buf_c);
         __syncthreads();
     };
     for (int tile = 0; tile < tiles; tile += 2)
     {
-        step(tile, st0);
+        step(tile, st1, Buf<0>{});
         if (tile + 1 < tiles)
-            step(tile + 1, st1);
+            step(tile + 1, st0, Buf<1>{});
     }
 
     if (!q_valid)
         return;
-    const float inv = 1.f / (row_sum + __shfl_xor(row_sum, 32));
+    const float inv = 1.f / sum_xor32(row_sum);
 
     // ---- store: lane holds features db*32 + 8*g + 4*half + [0,4) ----
     if constexpr (FUSED)
@@ -767,8 +810,9 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
 template <typename TIn, typename TOut, bool BF16, bool FUSED>
 static hipError_t launch_one(const AttentionLaunch& p, hipStream_t stream)
 {
-    // Row table: one 64-bit offset and one 32-bit coordinate word per row.
-    const size_t row_table = FUSED ? static_cast<size_t>(p.max_window_tokens) * 12 : 0;
+    // Row table: K and V row offsets and one coordinate word per row, padded
+    // to whole 64-row tiles.
+    const size_t row_table = static_cast<size_t>((p.max_window_tokens + 63) & ~63) * (2 * sizeof(long long) + 4);
     hipLaunchKernelGGL((window_attention_kernel<TIn, TOut, BF16, FUSED>), dim3(p.work_count), dim3(kThreads),
                        row_table, stream, p);
     return hipGetLastError();

@@ -785,6 +785,7 @@ int awa_window_attention(const awa_plan* plan, const awa_blob* input, const awa_
     p.windows = plan->dev.windows;
     p.work = plan->work;
     p.work_count = plan->work_count;
+    p.max_window_tokens = plan->max_window_tokens;
     p.heads = heads;
     p.text_tokens = plan->text_tokens;
     p.source_h = plan->source_h;
