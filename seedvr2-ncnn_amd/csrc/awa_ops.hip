@@ -152,40 +152,48 @@ __global__ void unpack_text_kernel(const int* text_positions, int window_count, 
 }
 
 // ---- Fused-path text mean over the per-window partials [nwin][T_x][H][d] ----
+// One thread per output element pair; the window loop is unrolled so that 8
+// loads per thread are in flight, and the sum keeps window order.
 __global__ void text_mean_kernel(const float* partials, int window_count, int text_tokens, int row_elems,
                                  void* out, long long out_row, int out_elemsize)
 {
-    const int groups = row_elems / 4;
-    const long long total = static_cast<long long>(text_tokens) * groups;
+    const int pairs = row_elems / 2;
+    const long long total = static_cast<long long>(text_tokens) * pairs;
     const long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (idx >= total)
         return;
-    const int k = static_cast<int>(idx / groups);
-    const int e = 4 * static_cast<int>(idx - static_cast<long long>(k) * groups);
-    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+    const int k = static_cast<int>(idx / pairs);
+    const int e = 2 * static_cast<int>(idx - static_cast<long long>(k) * pairs);
     const long long window_stride = static_cast<long long>(text_tokens) * row_elems;
     const float* src = partials + static_cast<long long>(k) * row_elems + e;
-    for (int w = 0; w < window_count; w++)
+    float sx = 0.f, sy = 0.f;
+    int w = 0;
+    for (; w + 8 <= window_count; w += 8)
     {
-        const float4 v = *reinterpret_cast<const float4*>(src + w * window_stride);
-        sum.x += v.x;
-        sum.y += v.y;
-        sum.z += v.z;
-        sum.w += v.w;
+        float2 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            v[j] = *reinterpret_cast<const float2*>(src + (w + j) * window_stride);
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+        {
+            sx += v[j].x;
+            sy += v[j].y;
+        }
+    }
+    for (; w < window_count; w++)
+    {
+        const float2 v = *reinterpret_cast<const float2*>(src + w * window_stride);
+        sx += v.x;
+        sy += v.y;
     }
     const float n = static_cast<float>(window_count);
     const long long o = k * out_row + e;
     if (out_elemsize == 4)
-    {
-        *reinterpret_cast<float4*>(static_cast<float*>(out) + o) = make_float4(sum.x / n, sum.y / n, sum.z / n, sum.w / n);
-    }
+        *reinterpret_cast<float2*>(static_cast<float*>(out) + o) = make_float2(sx / n, sy / n);
     else
-    {
-        uint16_t* dst = static_cast<uint16_t*>(out) + o;
-        const uint32_t lo = f32_to_bf16(sum.x / n) | (static_cast<uint32_t>(f32_to_bf16(sum.y / n)) << 16);
-        const uint32_t hi = f32_to_bf16(sum.z / n) | (static_cast<uint32_t>(f32_to_bf16(sum.w / n)) << 16);
-        *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
-    }
+        *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(out) + o) =
+            f32_to_bf16(sx / n) | (static_cast<uint32_t>(f32_to_bf16(sy / n)) << 16);
 }
 
 // ---- Generic window attention, any head_dim: one wave per (window-row, head) ----
@@ -315,7 +323,7 @@ hipError_t launch_text_mean(const float* partials, int window_count, int text_to
                             void* text_out, long long text_token_stride, int out_elemsize, hipStream_t stream)
 {
     const int row_elems = heads * head_dim;
-    const long long total = static_cast<long long>(text_tokens) * (row_elems / 4);
+    const long long total = static_cast<long long>(text_tokens) * (row_elems / 2);
     hipLaunchKernelGGL(text_mean_kernel, dim3(grid_for(total)), dim3(kBlock), 0, stream, partials, window_count,
                        text_tokens, row_elems, text_out, text_token_stride, out_elemsize);
     return hipGetLastError();
