@@ -296,15 +296,20 @@ __device__ __forceinline__ float sum_xor32(float x)
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <int N>
-using Buf = std::integral_constant<int, N>;
+// Bytes of the dynamic-LDS RoPE table: coords + 1 rows of 21 (cos, sin)
+// pairs, rounded up to 16 bytes.
+__host__ __device__ inline int rope_table_bytes(bool fused, int rope_coords)
+{
+    return fused ? ((rope_coords + 1) * kRopeRow * 4 + 15) & ~15 : 0;
+}
 
 template <typename TIn, typename TOut, bool BF16, bool FUSED>
-__global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const AttentionLaunch p)
+__global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const AttentionLaunch p)
 {
     // Key tile and LDS layout (pitches in elements; rows stay 16-byte aligned).
-    // 64-key tiles (two 32-key score blocks) on bf16 MFMA, 32 on fp32 MFMA;
-    // two buffers, so that tile t+1 is staged while tile t is computed.
+    // 64-key tiles (two 32-key score blocks) on bf16 MFMA, 32 on fp32 MFMA.
+    // The LDS footprint is kept under half a CU's LDS so that two workgroups
+    // share a CU and one's loads overlap the other's MFMA work.
     constexpr int KT = BF16 ? 64 : 32;
     constexpr int kKPitch = BF16 ? kHeadDim + 8 : kHeadDim + 4;
     constexpr int kVPitch = BF16 ? KT + 8 : KT + 4;
@@ -314,10 +319,13 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
     constexpr int kVBytes = kHeadDim * kVPitch * kElem;
     constexpr int kBlocks = KT / 32; // 32-key score blocks per tile
 
-    __shared__ __attribute__((aligned(16))) unsigned char k_lds[2 * kKBytes];
-    __shared__ __attribute__((aligned(16))) unsigned char v_lds[2 * kVBytes];
-    __shared__ __attribute__((aligned(16))) float rope_lds[FUSED ? kMaxRopeCoords * kRopeRow : 4];
-    extern __shared__ __attribute__((aligned(16))) unsigned char row_dyn[]; // row table
+    __shared__ __attribute__((aligned(16))) unsigned char k_lds[kKBytes];
+    __shared__ __attribute__((aligned(16))) unsigned char v_lds[kVBytes];
+    // Dynamic LDS: the RoPE table (fused mode; its coordinates plus an
+    // identity row), then the row table.
+    extern __shared__ __attribute__((aligned(16))) unsigned char dyn_lds[];
+    float* const rope_lds = reinterpret_cast<float*>(dyn_lds);
+    unsigned char* const row_dyn = dyn_lds + rope_table_bytes(FUSED, p.rope_coords);
 
     const WorkItem item = p.work[blockIdx.x];
     if (item.window < 0)
@@ -424,12 +432,15 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
     // ---- staging assignment ----
     // Loads are coalesced: 16 consecutive threads read the 16 chunks of 8
     // features of one row, so each load instruction covers 4 whole rows.
-    // Thread tid owns chunk kc = tid % 16 of K rows kr0 + 32 j and of V key
-    // group kr0: keys 2 kr0, 2 kr0 + 1 for bf16 MFMA (one 32-bit word of the
-    // transposed tile), key kr0 for fp32 MFMA.
-    constexpr int kKRows = KT / 32;
-    constexpr int kVKeys = BF16 ? 2 : 1;
+    // Thread tid owns chunk kc = tid % 16 of K rows kr0 + 16 j and of V key
+    // groups g = kr0 + 16 j: keys 2g, 2g + 1 for bf16 MFMA (one 32-bit word
+    // of the transposed tile), key g for fp32 MFMA.
+    constexpr int kRowsPerPass = kThreads / 16;     // rows one load instruction set covers
+    constexpr int kKRows = KT / kRowsPerPass;       // K rows per thread
+    constexpr int kVKeys = BF16 ? 2 : 1;            // keys per V word group
+    constexpr int kVGroups = KT / kVKeys / kRowsPerPass; // V key groups per thread
     static_assert(KT / kVKeys == 32, "32 V key groups per tile");
+    static_assert(kKRows * kRowsPerPass == KT && kVGroups * kRowsPerPass * kVKeys == KT, "staging split");
     const int kc = tid & 15;
     const int kr0 = tid >> 4;
     // RoPE of this thread's feature pairs 4kc .. 4kc+3: the coordinate of pair
@@ -446,34 +457,37 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
         rope_col[q] = axis < 3 ? 2 * (pair - axis * kRopePairs) : 0;
     }
 
-    // Two register stages: tile t+1 is written to LDS during step t and its
-    // registers then take the loads of tile t+3.
+    // One register stage: tile t+1's loads are in flight while tile t is
+    // computed.
     struct Stage
     {
         uint32_t k[kKRows * kRW];
-        uint32_t v[kVKeys * kRW];
+        uint32_t v[kVGroups * kVKeys * kRW];
     };
-    Stage st0, st1;
+    Stage st;
 
-    auto load_tile = [&](int tile, Stage& st) {
+    auto load_tile = [&](int tile) {
 #pragma unroll
         for (int j = 0; j < kKRows; j++)
-            load_raw8(reinterpret_cast<const TIn*>(load_base + row_k[tile * KT + kr0 + 32 * j]) + 8 * kc,
+            load_raw8(reinterpret_cast<const TIn*>(load_base + row_k[tile * KT + kr0 + kRowsPerPass * j]) + 8 * kc,
                       st.k + j * kRW);
 #pragma unroll
-        for (int j = 0; j < kVKeys; j++)
-            load_raw8(reinterpret_cast<const TIn*>(load_base + row_v[tile * KT + kVKeys * kr0 + j]) + 8 * kc,
-                      st.v + j * kRW);
+        for (int j = 0; j < kVGroups; j++)
+#pragma unroll
+            for (int i = 0; i < kVKeys; i++)
+                load_raw8(reinterpret_cast<const TIn*>(
+                              load_base + row_v[tile * KT + kVKeys * (kr0 + kRowsPerPass * j) + i]) +
+                              8 * kc,
+                          st.v + (j * kVKeys + i) * kRW);
     };
 
-    auto store_tile = [&](int tile, const Stage& st, auto buf_c) {
-        constexpr int buf = decltype(buf_c)::value;
-        unsigned char* const kb = k_lds + buf * kKBytes;
-        unsigned char* const vb = v_lds + buf * kVBytes;
+    auto store_tile = [&](int tile) {
+        unsigned char* const kb = k_lds;
+        unsigned char* const vb = v_lds;
 #pragma unroll
         for (int j = 0; j < kKRows; j++)
         {
-            const int row = kr0 + 32 * j;
+            const int row = kr0 + kRowsPerPass * j;
             float kv[8];
             raw_to_float8<TIn>(st.k + j * kRW, kv);
             if constexpr (FUSED)
@@ -504,15 +518,19 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
             }
         }
         // V transposed: Vt[d][key], keys swizzled in groups of 8 per feature chunk.
-        const int key = (kVKeys * kr0) ^ (8 * vt_swizzle<KT>(kc));
+#pragma unroll
+        for (int j = 0; j < kVGroups; j++)
+        {
+        const int key = (kVKeys * (kr0 + kRowsPerPass * j)) ^ (8 * vt_swizzle<KT>(kc));
+        const uint32_t* const sv = st.v + j * kVKeys * kRW;
 #pragma unroll
         for (int e = 0; e < 8; e++)
         {
             if constexpr (BF16)
             {
                 // One word = (key, key+1) at feature 8kc + e.
-                const uint32_t* a = st.v;
-                const uint32_t* b = st.v + kRW;
+                const uint32_t* a = sv;
+                const uint32_t* b = sv + kRW;
                 uint32_t word;
                 if constexpr (sizeof(TIn) == 2)
                     word = __builtin_amdgcn_perm(b[e >> 1], a[e >> 1], (e & 1) ? 0x07060302u : 0x05040100u);
@@ -524,23 +542,19 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
             {
                 float v;
                 if constexpr (sizeof(TIn) == 2)
-                    v = (e & 1) ? bf16_hi(st.v[e >> 1]) : bf16_lo(st.v[e >> 1]);
+                    v = (e & 1) ? bf16_hi(sv[e >> 1]) : bf16_lo(sv[e >> 1]);
                 else
-                    v = __uint_as_float(st.v[e]);
+                    v = __uint_as_float(sv[e]);
                 reinterpret_cast<float*>(vb)[(8 * kc + e) * kVPitch + key] = v;
             }
         }
+        }
     };
 
-    // ---- prologue: first two tiles' loads, the RoPE table into LDS (plus an
+    // ---- prologue: tile 0's loads, the RoPE table into LDS (plus an
     // identity row after the last coordinate), Q rotated and scaled in
-    // registers, tile 0 staged ----
-    load_tile(0, st0);
-    // With fp32 inputs the raw Q registers are twice as large; the second
-    // tile then follows once Q has been converted.
-    constexpr bool kEarlySecondTile = sizeof(TIn) == 2;
-    if (kEarlySecondTile && tiles > 1)
-        load_tile(1, st1);
+    // registers ----
+    load_tile(0);
     int q_ct = 0, q_ch = 0, q_cw = 0;
     if constexpr (FUSED)
     {
@@ -598,12 +612,6 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
         }
     }
 
-    if (!kEarlySecondTile && tiles > 1)
-        load_tile(1, st1);
-    store_tile(0, st0, Buf<0>{});
-    if (tiles > 2)
-        load_tile(2, st0);
-    __syncthreads();
 
     f32x16 o[4];
 #pragma unroll
@@ -617,8 +625,8 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
     const int krow = key_permute(col);
 
     // S^T = K Q^T of one tile: one 32x32 block per 32 keys; chains interleaved.
-    auto scores = [&](f32x16 (&s)[kBlocks], auto buf_c) {
-        constexpr int buf = decltype(buf_c)::value;
+    auto scores = [&](f32x16 (&s)[kBlocks]) {
+        constexpr int buf = 0;
 #pragma unroll
         for (int b = 0; b < kBlocks; b++)
 #pragma unroll
@@ -658,8 +666,8 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
 
     // Online softmax of one tile's scores, then O^T += V^T P^T.
     // Register i of score block b holds key 32b + 16*(i/8) + 8*half + i%8.
-    auto softmax_pv = [&](f32x16 (&s)[kBlocks], int tile, auto buf_c) {
-        constexpr int buf = decltype(buf_c)::value;
+    auto softmax_pv = [&](f32x16 (&s)[kBlocks], int tile) {
+        constexpr int buf = 0;
         if (tile == tiles - 1 && (L % KT))
         {
             const int key0 = tile * KT + 8 * half;
@@ -750,30 +758,21 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
         }
     };
 
-    // Step t: scores of tile t (LDS buffer t & 1); meanwhile tile t+1 goes
-    // from its registers into the other buffer and the registers take the
-    // loads of tile t+3; then softmax and PV of tile t. One barrier per step:
-    // it publishes tile t+1 and retires every read of buffer t & 1.
-    auto step = [&](int tile, Stage& next, auto buf_c) {
-        constexpr int buf = decltype(buf_c)::value;
-        f32x16 s[kBlocks];
-        if (wave_active)
-            scores(s, buf_c);
-        if (tile + 1 < tiles)
-        {
-            store_tile(tile + 1, next, Buf<buf ^ 1>{});
-            if (tile + 3 < tiles)
-                load_tile(tile + 3, next);
-        }
-        if (wave_active)
-            softmax_pv(s, tile, buf_c);
-        __syncthreads();
-    };
-    for (int tile = 0; tile < tiles; tile += 2)
+    // Step t: stage tile t into LDS, refill the registers with tile t+1's
+    // loads, then scores, softmax and PV of tile t.
+    for (int tile = 0; tile < tiles; tile++)
     {
-        step(tile, st1, Buf<0>{});
+        store_tile(tile);
+        __syncthreads();
         if (tile + 1 < tiles)
-            step(tile + 1, st0, Buf<1>{});
+            load_tile(tile + 1);
+        if (wave_active)
+        {
+            f32x16 s[kBlocks];
+            scores(s);
+            softmax_pv(s, tile);
+        }
+        __syncthreads();
     }
 
     if (!q_valid)
@@ -810,11 +809,12 @@ __global__ __launch_bounds__(kThreads, 1) void window_attention_kernel(const Att
 template <typename TIn, typename TOut, bool BF16, bool FUSED>
 static hipError_t launch_one(const AttentionLaunch& p, hipStream_t stream)
 {
-    // Row table: K and V row offsets and one coordinate word per row, padded
-    // to whole 64-row tiles.
+    // RoPE table, then the row table: K and V row offsets and one coordinate
+    // word per row, padded to whole 64-row tiles.
     const size_t row_table = static_cast<size_t>((p.max_window_tokens + 63) & ~63) * (2 * sizeof(long long) + 4);
+    const size_t dynamic_lds = rope_table_bytes(FUSED, p.rope_coords) + row_table;
     hipLaunchKernelGGL((window_attention_kernel<TIn, TOut, BF16, FUSED>), dim3(p.work_count), dim3(kThreads),
-                       row_table, stream, p);
+                       dynamic_lds, stream, p);
     return hipGetLastError();
 }
 

@@ -11,7 +11,7 @@ namespace awa
 
 constexpr int kHeadDim = 128;   // head_dim of the MFMA attention kernels
 constexpr int kRopeDim = 126;   // rope_dim of the fused kernel
-constexpr int kQueryWaves = 8;  // waves per attention workgroup, 32 query rows each
+constexpr int kQueryWaves = 4;  // waves per attention workgroup, 32 query rows each
 constexpr int kQueryRows = 32 * kQueryWaves; // query rows per workgroup
 constexpr int kMaxRopeCoords = 128; // RoPE coordinates the fused kernel holds in LDS
 constexpr int kMaxFusedWindowTokens = 1536; // rows of the fused kernel's LDS row table
