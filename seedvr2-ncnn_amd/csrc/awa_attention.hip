@@ -21,12 +21,15 @@
 // second kernel averages in window order. Packed mode reads a packed
 // [S][3H][d] blob and writes [S][H][d], for the staged WindowAttention layer.
 //
-// Per-tile VALU work is kept small: the window's row -> (grid position, RoPE
-// coordinates) table is built once per workgroup in LDS, the softmax scale is
-// folded into Q, masking only runs on a ragged last tile, and the output
-// accumulator is only rescaled when a row maximum grows by more than 2^8
-// (exact: numerator and denominator share the stale maximum). The next
-// tile's global loads are in flight while the current tile is computed.
+// Per-tile VALU work is kept small: the window's row -> (source offset, RoPE
+// coordinates) table is built once per workgroup in LDS (padded to whole
+// tiles, so staging loads need no bounds checks), the softmax scale is folded
+// into Q, masking only runs on a ragged last tile, and the output accumulator
+// is only rescaled when a row maximum grows by more than 2^8 (exact:
+// numerator and denominator share the stale maximum). The next tile's global
+// loads are in flight while the current tile is computed, and the LDS
+// footprint lets two workgroups share a CU, so one's memory waits overlap the
+// other's MFMA work.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -131,67 +134,6 @@ __device__ __forceinline__ void rope_pair_fma(float& x0, float& x1, float c, flo
     const float b = x1;
     x0 = fmaf(a, c, -(b * s));
     x1 = fmaf(b, c, a * s);
-}
-
-__device__ __forceinline__ void rope_pair(float& x0, float& x1, const float* cs)
-{
-    const float2 t = *reinterpret_cast<const float2*>(cs);
-    rope_pair_cs(x0, x1, t.x, t.y);
-}
-
-// Rotates kPairs consecutive feature pairs starting at pair kPair0 (both
-// compile-time, so each pair's axis and table column fold to constants) of a
-// row with RoPE coordinates (ct, ch, cw). Pair p belongs to axis p / 21;
-// pairs at or beyond rope_dim / 2 are left unchanged.
-template <int kPair0, int kPairs>
-__device__ __forceinline__ void rope_fixed(float* v, int ct, int ch, int cw, const float* table)
-{
-#pragma unroll
-    for (int q = 0; q < kPairs; q++)
-    {
-        const int pair = kPair0 + q;
-        if (2 * pair < kRopeDim)
-        {
-            const int axis = pair / kRopePairs;
-            const int coord = axis == 0 ? ct : (axis == 1 ? ch : cw);
-            rope_pair(v[2 * q], v[2 * q + 1], table + coord * kRopeRow + 2 * (pair - axis * kRopePairs));
-        }
-    }
-}
-
-// rope_fixed for a run whose first pair index is a multiple of kPairs known
-// only at run time (slice = first pair / kPairs, 0 <= slice < 64 / kPairs).
-template <int kPairs>
-__device__ __forceinline__ void rope_slice(float* v, int slice, int ct, int ch, int cw, const float* table)
-{
-    static_assert(kPairs == 4 || kPairs == 8 || kPairs == 16, "slice width");
-    switch (slice)
-    {
-#define AWA_ROPE_CASE(n)                                                            \
-    case n:                                                                         \
-        if constexpr ((n + 1) * kPairs <= 64)                                       \
-            rope_fixed<(n * kPairs) % 64, kPairs>(v, ct, ch, cw, table);            \
-        break;
-        AWA_ROPE_CASE(0)
-        AWA_ROPE_CASE(1)
-        AWA_ROPE_CASE(2)
-        AWA_ROPE_CASE(3)
-        AWA_ROPE_CASE(4)
-        AWA_ROPE_CASE(5)
-        AWA_ROPE_CASE(6)
-        AWA_ROPE_CASE(7)
-        AWA_ROPE_CASE(8)
-        AWA_ROPE_CASE(9)
-        AWA_ROPE_CASE(10)
-        AWA_ROPE_CASE(11)
-        AWA_ROPE_CASE(12)
-        AWA_ROPE_CASE(13)
-        AWA_ROPE_CASE(14)
-        AWA_ROPE_CASE(15)
-#undef AWA_ROPE_CASE
-    default:
-        break;
-    }
 }
 
 // Row table entry of window-local row i: video rows store their local
@@ -555,13 +497,10 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
     // identity row after the last coordinate), Q rotated and scaled in
     // registers ----
     load_tile(0);
-    int q_ct = 0, q_ch = 0, q_cw = 0;
+    uint32_t q_code = 0; // RoPE coordinate word of this lane's query row
     if constexpr (FUSED)
     {
-        const uint32_t code = row_code[q_row];
-        q_ct = static_cast<int>(code & 255u);
-        q_ch = static_cast<int>((code >> 8) & 255u);
-        q_cw = static_cast<int>((code >> 16) & 255u);
+        q_code = row_code[q_row];
         const int n = p.rope_coords * kRopeRow;
 #pragma unroll
         for (int j = 0; j < kRopePerThread; j++)
@@ -587,11 +526,26 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
         raw_to_float8<TIn>(qraw + c * kRW, v);
         if constexpr (FUSED)
         {
-            // 4 pairs from pair 8c + 4*half (bf16) or 32*half + 4c (fp32).
-            if constexpr (BF16)
-                rope_slice<4>(v, 2 * c + half, q_ct, q_ch, q_cw, rope_lds);
-            else
-                rope_slice<4>(v, 8 * half + c, q_ct, q_ch, q_cw, rope_lds);
+            // 4 pairs from pair 8c + 4*half (bf16) or 32*half + 4c (fp32):
+            // their axes and table columns are compile-time for either half,
+            // one select picks the lane's.
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+            {
+                const int p0 = (BF16 ? 8 * c : 4 * c) + q;
+                const int p1 = (BF16 ? 8 * c + 4 : 32 + 4 * c) + q;
+                const int ax0 = 2 * p0 < kRopeDim ? p0 / kRopePairs : 3;
+                const int ax1 = 2 * p1 < kRopeDim ? p1 / kRopePairs : 3;
+                const int col0 = ax0 < 3 ? 2 * (p0 - ax0 * kRopePairs) : 0;
+                const int col1 = ax1 < 3 ? 2 * (p1 - ax1 * kRopePairs) : 0;
+                const uint32_t coord = (q_code >> (half ? 8 * ax1 : 8 * ax0)) & 255u;
+                const float2 t =
+                    *reinterpret_cast<const float2*>(rope_lds + coord * kRopeRow + (half ? col1 : col0));
+                if constexpr (BF16)
+                    rope_pair_fma(v[2 * q], v[2 * q + 1], t.x, t.y);
+                else
+                    rope_pair_cs(v[2 * q], v[2 * q + 1], t.x, t.y);
+            }
         }
 #pragma unroll
         for (int e = 0; e < 8; e++)
