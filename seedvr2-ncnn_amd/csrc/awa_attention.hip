@@ -187,20 +187,23 @@ __device__ __forceinline__ RowRef decode_row(uint32_t e, int t0, int h0, int w0,
     return r;
 }
 
-// Row order of a 32-key block as read by the S^T MFMA: swap bits 2 and 3.
+// Key order of a 32-key block in the K tile: key m is stored at row
+// key_permute(m) (bits 2 and 3 swapped), so that the S^T MFMA, reading rows
+// in lane order (conflict-free), sees the keys in the order the PV operand
+// layout needs.
 __device__ __forceinline__ int key_permute(int m)
 {
     return (m & ~0xC) | ((m & 4) << 1) | ((m & 8) >> 1);
 }
 
 // Key swizzle of the transposed V tile: row d of Vt stores key k at column
-// k ^ (8 * vt_swizzle(d / 8)). Groups of 8 keys stay contiguous (one 16-byte
-// MFMA operand read), while the staging writes of the 16 feature chunks land
-// in distinct LDS banks.
+// k ^ (8 * vt_swizzle(d)). Groups of 8 keys stay contiguous (one 16-byte MFMA
+// operand read); the PV reads of 16 consecutive rows cover every LDS bank
+// once, with 32 or 64 banks.
 template <int KT>
-__device__ __forceinline__ int vt_swizzle(int chunk)
+__device__ __forceinline__ int vt_swizzle(int d)
 {
-    return (chunk + (chunk >> 3)) & (KT / 8 - 1);
+    return (d >> 4) & (KT / 8 - 1);
 }
 
 __device__ __forceinline__ void store4(float* dst, float a, float b, float c, float d)
@@ -430,6 +433,7 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
         for (int j = 0; j < kKRows; j++)
         {
             const int row = kr0 + kRowsPerPass * j;
+            const int lds_row = (row & ~31) | key_permute(row & 31);
             float kv[8];
             raw_to_float8<TIn>(st.k + j * kRW, kv);
             if constexpr (FUSED)
@@ -448,13 +452,13 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
             }
             if constexpr (BF16)
             {
-                uint16_t* ks = reinterpret_cast<uint16_t*>(kb) + row * kKPitch + 8 * kc;
+                uint16_t* ks = reinterpret_cast<uint16_t*>(kb) + lds_row * kKPitch + 8 * kc;
                 *reinterpret_cast<uint4*>(ks) = make_uint4(cvt_pk_bf16(kv[0], kv[1]), cvt_pk_bf16(kv[2], kv[3]),
                                                            cvt_pk_bf16(kv[4], kv[5]), cvt_pk_bf16(kv[6], kv[7]));
             }
             else
             {
-                float* ks = reinterpret_cast<float*>(kb) + row * kKPitch + 8 * kc;
+                float* ks = reinterpret_cast<float*>(kb) + lds_row * kKPitch + 8 * kc;
                 *reinterpret_cast<float4*>(ks) = make_float4(kv[0], kv[1], kv[2], kv[3]);
                 *reinterpret_cast<float4*>(ks + 4) = make_float4(kv[4], kv[5], kv[6], kv[7]);
             }
@@ -463,7 +467,7 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
 #pragma unroll
         for (int j = 0; j < kVGroups; j++)
         {
-        const int key = (kVKeys * (kr0 + kRowsPerPass * j)) ^ (8 * vt_swizzle<KT>(kc));
+        const int key = (kVKeys * (kr0 + kRowsPerPass * j)) ^ (8 * vt_swizzle<KT>(8 * kc));
         const uint32_t* const sv = st.v + j * kVKeys * kRW;
 #pragma unroll
         for (int e = 0; e < 8; e++)
@@ -576,7 +580,7 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
     float row_max = -INFINITY; // running maximum (log2 domain), possibly stale by < 2^8
     float row_sum = 0.f;       // partial sum over this lane's keys
 
-    const int krow = key_permute(col);
+    const int krow = col; // K rows are stored key-permuted
 
     // S^T = K Q^T of one tile: one 32x32 block per 32 keys; chains interleaved.
     auto scores = [&](f32x16 (&s)[kBlocks]) {
@@ -679,7 +683,7 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
             {
                 const int d = db * 32 + col;
                 const uint16_t* vrow = vt + d * kVPitch;
-                const int swz = 8 * vt_swizzle<KT>(d >> 3);
+                const int swz = 8 * vt_swizzle<KT>(d);
                 bf16x8 va[2 * kBlocks];
 #pragma unroll
                 for (int j = 0; j < 2 * kBlocks; j++)
@@ -697,7 +701,7 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
             {
                 const int d = db * 32 + col;
                 const float* vrow = vt + d * kVPitch;
-                const int swz = 8 * vt_swizzle<KT>(d >> 3);
+                const int swz = 8 * vt_swizzle<KT>(d);
 #pragma unroll
                 for (int g = 0; g < 4; g++)
                 {
