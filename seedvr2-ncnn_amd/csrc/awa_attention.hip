@@ -608,17 +608,25 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
         }
         else
         {
-            // One chain over this lane's 64 features (32x32x2 f32 MFMAs).
+            // Two interleaved chains over this lane's 64 features (32x32x2
+            // f32 MFMAs), so that consecutive MFMAs are independent.
             const float* ks = reinterpret_cast<const float*>(k_lds + buf * kKBytes) + krow * kKPitch + 64 * half;
+            f32x16 s1;
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                s1[i] = 0.f;
 #pragma unroll
             for (int c4 = 0; c4 < 16; c4++)
             {
                 const float4 ka = *reinterpret_cast<const float4*>(ks + 4 * c4);
                 s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.x, qf[4 * c4 + 0], s[0], 0, 0, 0);
-                s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.y, qf[4 * c4 + 1], s[0], 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.y, qf[4 * c4 + 1], s1, 0, 0, 0);
                 s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.z, qf[4 * c4 + 2], s[0], 0, 0, 0);
-                s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.w, qf[4 * c4 + 3], s[0], 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.w, qf[4 * c4 + 3], s1, 0, 0, 0);
             }
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                s[0][i] += s1[i];
         }
     };
 
@@ -677,41 +685,53 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
                     pb[2 * b][e] = static_cast<__bf16>(s[b][e]);
                     pb[2 * b + 1][e] = static_cast<__bf16>(s[b][8 + e]);
                 }
+            // The four output chains are interleaved: consecutive MFMAs are
+            // independent.
             const uint16_t* vt = reinterpret_cast<const uint16_t*>(v_lds + buf * kVBytes);
 #pragma unroll
-            for (int db = 0; db < 4; db++)
+            for (int j = 0; j < 2 * kBlocks; j++)
             {
-                const int d = db * 32 + col;
-                const uint16_t* vrow = vt + d * kVPitch;
-                const int swz = 8 * vt_swizzle<KT>(d);
-                bf16x8 va[2 * kBlocks];
+                bf16x8 va[4];
 #pragma unroll
-                for (int j = 0; j < 2 * kBlocks; j++)
-                    va[j] = *reinterpret_cast<const bf16x8*>(vrow + ((8 * half + 16 * j) ^ swz));
+                for (int db = 0; db < 4; db++)
+                {
+                    const int d = db * 32 + col;
+                    va[db] = *reinterpret_cast<const bf16x8*>(vt + d * kVPitch +
+                                                              ((8 * half + 16 * j) ^ (8 * vt_swizzle<KT>(d))));
+                }
 #pragma unroll
-                for (int j = 0; j < 2 * kBlocks; j++)
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[j], pb[j], o[db], 0, 0, 0);
+                for (int db = 0; db < 4; db++)
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[db], pb[j], o[db], 0, 0, 0);
             }
         }
         else
         {
+            // The four output chains are interleaved: consecutive MFMAs are
+            // independent.
             const float* vt = reinterpret_cast<const float*>(v_lds + buf * kVBytes);
 #pragma unroll
-            for (int db = 0; db < 4; db++)
+            for (int g = 0; g < 4; g++)
             {
-                const int d = db * 32 + col;
-                const float* vrow = vt + d * kVPitch;
-                const int swz = 8 * vt_swizzle<KT>(d);
+                float4 va[4];
 #pragma unroll
-                for (int g = 0; g < 4; g++)
+                for (int db = 0; db < 4; db++)
                 {
-                    const float4 va =
-                        *reinterpret_cast<const float4*>(vrow + ((16 * (g >> 1) + 8 * half + 4 * (g & 1)) ^ swz));
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.x, s[0][4 * g + 0], o[db], 0, 0, 0);
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.y, s[0][4 * g + 1], o[db], 0, 0, 0);
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.z, s[0][4 * g + 2], o[db], 0, 0, 0);
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.w, s[0][4 * g + 3], o[db], 0, 0, 0);
+                    const int d = db * 32 + col;
+                    va[db] = *reinterpret_cast<const float4*>(
+                        vt + d * kVPitch + ((16 * (g >> 1) + 8 * half + 4 * (g & 1)) ^ (8 * vt_swizzle<KT>(d))));
                 }
+#pragma unroll
+                for (int db = 0; db < 4; db++)
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va[db].x, s[0][4 * g + 0], o[db], 0, 0, 0);
+#pragma unroll
+                for (int db = 0; db < 4; db++)
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va[db].y, s[0][4 * g + 1], o[db], 0, 0, 0);
+#pragma unroll
+                for (int db = 0; db < 4; db++)
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va[db].z, s[0][4 * g + 2], o[db], 0, 0, 0);
+#pragma unroll
+                for (int db = 0; db < 4; db++)
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va[db].w, s[0][4 * g + 3], o[db], 0, 0, 0);
             }
         }
     };
