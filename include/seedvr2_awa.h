@@ -197,8 +197,15 @@ void awa_stack_destroy(awa_stack* stack);
 int awa_stack_run(awa_stack* stack, void* const* video_qkv, void* const* text_qkv, void* const* video_out,
                   void* const* text_out, void* stream);
 /* Optional per-block timing (the reference's --profile surface): when enabled
- * each run records events around every block's attention kernel. */
+ * each run records events around every block's attention kernel (and runs
+ * eagerly). */
 int awa_stack_set_profiling(awa_stack* stack, int enabled);
+/* Step replay through a HIP graph (default on; no reference counterpart, the
+ * reference submits one command buffer per block): the first run with a new
+ * set of block pointers runs eagerly and records the step, later runs with
+ * the same pointers replay it with one launch. Runs on the null stream are
+ * always eager. */
+int awa_stack_set_graph(awa_stack* stack, int enabled);
 /* After a profiled run has completed: milliseconds of each block's attention
  * kernel and of the block's layer (attention kernel + text mean). */
 int awa_stack_block_times(const awa_stack* stack, float* attention_ms, float* block_ms);

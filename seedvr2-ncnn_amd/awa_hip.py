@@ -35,7 +35,7 @@ EXPORTED_SYMBOLS = (
     "awa_plan_info_get", "awa_plan_windows", "awa_plan_sequence_index", "awa_plan_cu_seqlens",
     "awa_plan_video_positions", "awa_plan_text_positions", "awa_plan_rope_table", "awa_plan_upload",
     "awa_qkv_shape", "awa_forward", "awa_pack", "awa_mmrope", "awa_window_attention", "awa_unpack", "awa_cast",
-    "awa_stack_create", "awa_stack_destroy", "awa_stack_run", "awa_stack_set_profiling", "awa_stack_block_times",
+    "awa_stack_create", "awa_stack_destroy", "awa_stack_run", "awa_stack_set_profiling", "awa_stack_set_graph", "awa_stack_block_times",
     "awa_stack_block_flops",
 )
 
@@ -375,6 +375,10 @@ class AttentionStack:
 
     def set_profiling(self, enabled: bool) -> None:
         check(lib().awa_stack_set_profiling(ctypes.c_void_p(self.handle), int(enabled)), "awa_stack_set_profiling")
+
+    def set_graph(self, enabled: bool) -> None:
+        """Replay steps through a captured HIP graph (default on)."""
+        check(lib().awa_stack_set_graph(ctypes.c_void_p(self.handle), int(enabled)), "awa_stack_set_graph")
 
     def block_times(self):
         att = (ctypes.c_float * self.blocks)()

@@ -5,6 +5,10 @@
 // window partition alternates unshifted / shifted by block parity, so the
 // stack holds two plans. At the first bf16 block the previous block's outputs
 // are converted to bf16 once (the reference's convert_precision_gpu calls).
+//
+// A step is 32 layers of 2 kernels each on one stream. With graphs enabled
+// (the default) the step is captured once per set of block pointers and
+// replayed with a single graph launch; the capture only holds kernel nodes.
 #include <hip/hip_runtime.h>
 
 #include <new>
@@ -22,6 +26,10 @@ struct awa_stack
     bool profiling = false;
     std::vector<hipEvent_t> events; // 3 per block: start, after attention, end
     std::vector<double> flops;
+    // Captured step: valid for the block pointers it was recorded with.
+    bool use_graph = true;
+    hipGraphExec_t graph = nullptr;
+    std::vector<void*> graph_key;
 };
 
 namespace
@@ -63,6 +71,10 @@ void release(awa_stack* s)
     for (hipEvent_t e : s->events)
         (void)hipEventDestroy(e);
     s->events.clear();
+    if (s->graph)
+        (void)hipGraphExecDestroy(s->graph);
+    s->graph = nullptr;
+    s->graph_key.clear();
 }
 
 } // namespace
@@ -155,13 +167,14 @@ int awa_stack_set_profiling(awa_stack* stack, int enabled)
     return AWA_OK;
 }
 
-int awa_stack_run(awa_stack* stack, void* const* video_qkv, void* const* text_qkv, void* const* video_out,
-                  void* const* text_out, void* stream)
+namespace
 {
-    if (!stack || !video_qkv || !text_qkv || !video_out || !text_out)
-        return fail(AWA_ERR_INVALID, "null argument");
+
+// Enqueues one step on s (eager, or into a capture).
+int enqueue_step(awa_stack* stack, void* const* video_qkv, void* const* text_qkv, void* const* video_out,
+                 void* const* text_out, hipStream_t s)
+{
     const awa_stack_desc& d = stack->desc;
-    hipStream_t s = static_cast<hipStream_t>(stream);
     awa_plan_info info{};
     awa_plan_info_get(stack->plans[0], &info);
     const int H = d.heads, D = d.head_dim;
@@ -196,6 +209,65 @@ int awa_stack_run(awa_stack* stack, void* const* video_qkv, void* const* text_qk
         if (ev && hipEventRecord(ev[2], s) != hipSuccess)
             return fail(AWA_ERR_DEVICE, "hipEventRecord failed");
     }
+    return AWA_OK;
+}
+
+} // namespace
+
+int awa_stack_run(awa_stack* stack, void* const* video_qkv, void* const* text_qkv, void* const* video_out,
+                  void* const* text_out, void* stream)
+{
+    if (!stack || !video_qkv || !text_qkv || !video_out || !text_out)
+        return fail(AWA_ERR_INVALID, "null argument");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // Eager when profiling (per-block events), on the null stream (which
+    // cannot be captured) or with graphs disabled.
+    if (stack->profiling || !stack->use_graph || !s)
+        return enqueue_step(stack, video_qkv, text_qkv, video_out, text_out, s);
+    const int n = stack->desc.blocks;
+    std::vector<void*> key;
+    key.reserve(4 * static_cast<size_t>(n));
+    for (void* const* arr : {video_qkv, text_qkv, video_out, text_out})
+        key.insert(key.end(), arr, arr + n);
+    if (stack->graph && key == stack->graph_key)
+        return hipGraphLaunch(stack->graph, s) == hipSuccess ? AWA_OK : fail(AWA_ERR_DEVICE, "hipGraphLaunch failed");
+    // New pointers: run eagerly (which also creates the plans' device
+    // workspaces outside any capture), then record the step for next time.
+    int rc = enqueue_step(stack, video_qkv, text_qkv, video_out, text_out, s);
+    if (rc != AWA_OK)
+        return rc;
+    if (stack->graph)
+    {
+        (void)hipGraphExecDestroy(stack->graph);
+        stack->graph = nullptr;
+        stack->graph_key.clear();
+    }
+    hipGraph_t g = nullptr;
+    if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess)
+        return fail(AWA_ERR_DEVICE, "hipStreamBeginCapture failed");
+    rc = enqueue_step(stack, video_qkv, text_qkv, video_out, text_out, s);
+    const hipError_t end = hipStreamEndCapture(s, &g);
+    if (rc != AWA_OK || end != hipSuccess)
+    {
+        if (g)
+            (void)hipGraphDestroy(g);
+        return rc != AWA_OK ? rc : fail(AWA_ERR_DEVICE, "hipStreamEndCapture failed");
+    }
+    hipGraphExec_t exec = nullptr;
+    const hipError_t inst = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (inst != hipSuccess)
+        return fail(AWA_ERR_DEVICE, "hipGraphInstantiate failed");
+    stack->graph = exec;
+    stack->graph_key = std::move(key);
+    return AWA_OK;
+}
+
+int awa_stack_set_graph(awa_stack* stack, int enabled)
+{
+    if (!stack)
+        return fail(AWA_ERR_INVALID, "null stack");
+    stack->use_graph = enabled != 0;
     return AWA_OK;
 }
 

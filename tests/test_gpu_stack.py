@@ -1,0 +1,105 @@
+"""The DiT attention stack (awa_stack_*): per-block fp32 / bf16 dispatch, the
+unshifted / shifted alternation and the block-9-style precision switch
+(src/dit/dit_stack.cpp:497-565, :931-982; tools/reference/dit_stack.py:75-79),
+eager and replayed through a captured HIP graph."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import awa_hip as A
+import oracle as O
+from awa_cases import abs_err, qkv_inputs, rel_err
+
+pytestmark = pytest.mark.gpu
+
+GRID = (2, 16, 16)
+WINDOWS = (1, 8, 8)
+TEXT = 64
+HEADS = 2
+D = 128
+BLOCKS = 4
+PREFIX = 2  # blocks 0, 1 fp32; 2, 3 bf16
+
+
+class StackData:
+    """Per-block inputs (host copies as the values the device holds) and
+    device buffers for the outputs."""
+
+    def __init__(self):
+        self.n = GRID[0] * GRID[1] * GRID[2]
+        self.inputs, self.buffers = [], []
+        for b in range(BLOCKS):
+            es = 4 if b < PREFIX else 2
+            g = O.Geometry(*GRID, *WINDOWS, TEXT, bool(b & 1))
+            video, text = qkv_inputs(g, HEADS, D, 20260901 + b)
+            if es == 2:
+                video, text = O.round_bf16(video), O.round_bf16(text)
+            bufs = [A.DeviceBuffer(video.size * es), A.DeviceBuffer(text.size * es),
+                    A.DeviceBuffer(self.n * HEADS * D * es), A.DeviceBuffer(TEXT * HEADS * D * es)]
+            for buf, x in zip(bufs[:2], (video, text)):
+                buf.upload(x.astype(np.float32) if es == 4 else A.f32_to_bf16_bits(x))
+            self.inputs.append((g, video, text))
+            self.buffers.append(bufs)
+
+    def pointers(self):
+        return [[bufs[i].ptr for bufs in self.buffers] for i in range(4)]
+
+    def outputs(self):
+        out = []
+        for b, bufs in enumerate(self.buffers):
+            if b < PREFIX:
+                v = bufs[2].download((self.n, HEADS, D), np.float32)
+                t = bufs[3].download((TEXT, HEADS, D), np.float32)
+            else:
+                v = A.bf16_bits_to_f32(bufs[2].download((self.n, HEADS, D), np.uint16))
+                t = A.bf16_bits_to_f32(bufs[3].download((TEXT, HEADS, D), np.uint16))
+            out.append((v, t))
+        return out
+
+    def zero_outputs(self, stream):
+        for bufs in self.buffers:
+            bufs[2].zero(stream)
+            bufs[3].zero(stream)
+
+
+def test_stack_blocks_match_oracle(gpu):
+    print("case stack 4 blocks 2x16x16 eager", flush=True)
+    data = StackData()
+    stack = A.AttentionStack(*GRID, *WINDOWS, TEXT, BLOCKS, PREFIX, HEADS, D)
+    stack.set_graph(False)
+    stream = A.Stream()
+    stack.run(*data.pointers(), stream)
+    stream.synchronize()
+    for b, ((g, video, text), (v, t)) in enumerate(zip(data.inputs, data.outputs())):
+        assert g.shifted == bool(b & 1)
+        ref_v, ref_t = O.awa_layer(g, video, text, HEADS, D)
+        if b < PREFIX:
+            assert abs_err(v, ref_v) <= 1e-4 and abs_err(t, ref_t) <= 1e-4, b
+        else:
+            assert rel_err(v, ref_v) <= 2e-2 and rel_err(t, ref_t) <= 2e-2, b
+    stack.destroy()
+    stream.destroy()
+
+
+def test_stack_graph_replays_match_eager(gpu):
+    print("case stack 4 blocks 2x16x16 graph replays", flush=True)
+    data = StackData()
+    stack = A.AttentionStack(*GRID, *WINDOWS, TEXT, BLOCKS, PREFIX, HEADS, D)
+    stream = A.Stream()
+    stack.set_graph(False)
+    stack.run(*data.pointers(), stream)
+    stream.synchronize()
+    eager = data.outputs()
+    stack.set_graph(True)
+    # First graph-mode run records the step (and runs it eagerly); the next
+    # ones replay it. Outputs are cleared by eager kernels between replays.
+    for replay in range(4):
+        data.zero_outputs(stream)
+        stack.run(*data.pointers(), stream)
+        stream.synchronize()
+        for b, ((v, t), (ev, et)) in enumerate(zip(data.outputs(), eager)):
+            assert np.array_equal(v, ev) and np.array_equal(t, et), (replay, b)
+    stack.destroy()
+    stream.destroy()
