@@ -116,3 +116,45 @@ def test_bf16_output_rounding(gpu):
     v16, t16 = run_fused(g, video, text, A.COMPUTE_F32, out_elem=2)
     np.testing.assert_array_equal(v16, bf16_round(v32))
     np.testing.assert_array_equal(t16, bf16_round(t32))
+
+
+# The benchmark workloads themselves: 33 frames 256x256 (9x16x16), 9 frames
+# 512x512 (9x32x32) and 121 frames 256x256 (31x16x16, windows of up to 320
+# rows and a ragged temporal remainder), both partitions, both precisions.
+@pytest.mark.parametrize("name", ["clip_9x16x16", "clip_9x32x32", "clip_31x16x16"])
+@pytest.mark.parametrize("shifted", [False, True])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_benchmark_shapes(gpu, name, shifted, bf16):
+    heads = 20 if name == "clip_9x16x16" else 4
+    g = geometry(CONFIGS[name], shifted)
+    print(f"case {name} shifted={shifted} bf16={bf16} heads={heads}", flush=True)
+    video, text = qkv_inputs(g, heads, HEAD_DIM, 20260825)
+    if bf16:
+        video, text = bf16_round(video), bf16_round(text)
+    ref_v, ref_t = O.awa_layer(g, video, text, heads, HEAD_DIM)
+    if bf16:
+        got_v, got_t = run_fused(g, video, text, A.COMPUTE_BF16, in_elem=2, out_elem=2)
+        assert rel_err(got_v, ref_v) <= BF16_RTOL and rel_err(got_t, ref_t) <= BF16_RTOL
+    else:
+        got_v, got_t = run_fused(g, video, text, A.COMPUTE_F32)
+        assert abs_err(got_v, ref_v) <= FP32_ATOL and abs_err(got_t, ref_t) <= FP32_ATOL
+
+
+# Every input / output element size with either arithmetic, including fp32
+# QKV into bf16 arithmetic (how QKV reaches AWA in the reference's BF16
+# blocks: src/dit/dit_precision.cpp:22-142).
+@pytest.mark.parametrize("in_elem", [4, 2])
+@pytest.mark.parametrize("out_elem", [4, 2])
+@pytest.mark.parametrize("compute", [A.COMPUTE_F32, A.COMPUTE_BF16])
+def test_precision_combinations(gpu, in_elem, out_elem, compute):
+    g = geometry((3, 11, 13, 2, 3, 3, 5), True)
+    print(f"case precision in={in_elem} out={out_elem} compute={compute}", flush=True)
+    video, text = qkv_inputs(g, 3, HEAD_DIM, 20260826)
+    if in_elem == 2:
+        video, text = bf16_round(video), bf16_round(text)
+    ref_v, ref_t = O.awa_layer(g, video, text, 3, HEAD_DIM)
+    got_v, got_t = run_fused(g, video, text, compute, in_elem=in_elem, out_elem=out_elem)
+    if compute == A.COMPUTE_F32 and out_elem == 4:
+        assert abs_err(got_v, ref_v) <= FP32_ATOL and abs_err(got_t, ref_t) <= FP32_ATOL
+    else:
+        assert rel_err(got_v, ref_v) <= BF16_RTOL and rel_err(got_t, ref_t) <= BF16_RTOL
