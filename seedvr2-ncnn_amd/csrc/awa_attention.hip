@@ -1,10 +1,11 @@
 // Window attention kernels for gfx950 (CDNA4).
 //
-// One workgroup = 4 waves = 128 query rows of one (window, head). Each wave
-// owns 32 query rows and computes the transposed score tile S^T = K Q^T with
-// 32x32 MFMAs, so that a lane holds one query column: the online-softmax
-// statistics of a query live in two lanes (lane and lane^32), and the
-// rescale of the output accumulator O^T = V^T P^T is lane-local.
+// Each wave owns 32 query rows of one (window, head) and computes the
+// transposed score tile S^T = K Q^T with 32x32 MFMAs, so that a lane holds one
+// query column: the online-softmax statistics of a query live in two lanes
+// (lane and lane^32), and the rescale of the output accumulator O^T = V^T P^T
+// is lane-local. A workgroup is 4 waves (128 query rows; bf16 MFMA) or 8
+// waves (256 query rows; fp32 MFMA), see the variants below.
 //
 // K and V tiles (64 keys for bf16, 32 for fp32) are staged through LDS (K
 // row-major, V transposed so that the PV operand reads are contiguous in the
@@ -24,12 +25,10 @@
 // Per-tile VALU work is kept small: the window's row -> (source offset, RoPE
 // coordinates) table is built once per workgroup in LDS (padded to whole
 // tiles, so staging loads need no bounds checks), the softmax scale is folded
-// into Q, masking only runs on a ragged last tile, and the output accumulator
-// is only rescaled when a row maximum grows by more than 2^8 (exact:
-// numerator and denominator share the stale maximum). The next tile's global
-// loads are in flight while the current tile is computed, and the LDS
-// footprint lets two workgroups share a CU, so one's memory waits overlap the
-// other's MFMA work.
+// into Q, masking only runs on a ragged last tile, and (bf16) the output
+// accumulator is only rescaled when a row maximum grows by more than 2^8
+// (exact: numerator and denominator share the stale maximum). The next
+// tile's global loads are in flight while the current tile is computed.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -46,7 +45,6 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kThreads = 64 * kQueryWaves;
 constexpr int kRopePairs = kRopeDim / 6; // 21 pairs per axis
 constexpr int kRopeRow = 2 * kRopePairs; // floats per coordinate in the table
 constexpr float kRescaleThreshold = 8.f; // log2 units
@@ -248,13 +246,26 @@ __host__ __device__ inline int rope_table_bytes(bool fused, int rope_coords)
     return fused ? ((rope_coords + 1) * kRopeRow * 4 + 15) & ~15 : 0;
 }
 
-template <typename TIn, typename TOut, bool BF16, bool FUSED>
-__global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const AttentionLaunch p)
+// Variants (AttentionLaunch::variant):
+//   kVariantNarrow: 4 waves (128 query rows), single-buffered K/V tiles of 64
+//     (bf16) or 32 (fp32) keys, two barriers per tile; the LDS footprint stays
+//     under half a CU's, so that two workgroups share a CU.
+//   kVariantWidePipe: 8 waves (256 query rows), double-buffered tiles and a
+//     software pipeline with one barrier per tile: the scores of tile t+1 and
+//     the PV of tile t are issued next to the softmax of tile t and the
+//     staging of the next tiles.
+template <typename TIn, typename TOut, bool BF16, bool FUSED, int VARIANT>
+__global__ __launch_bounds__(VARIANT == kVariantWidePipe ? 512 : 256,
+                             VARIANT == kVariantWidePipe ? 1 : 2) void window_attention_kernel(const AttentionLaunch p)
 {
+    constexpr bool WIDE = VARIANT == kVariantWidePipe;
+    constexpr bool PIPE = WIDE;
+    constexpr int kThreads = WIDE ? 512 : 256;
+    constexpr int kQueryRows = kThreads / 2; // 32 rows per wave
+    static_assert(kQueryRows == (WIDE ? awa::kWideQueryRows : awa::kQueryRows), "work items match the variant");
+    constexpr int kBufs = PIPE ? 2 : 1;
     // Key tile and LDS layout (pitches in elements; rows stay 16-byte aligned).
     // 64-key tiles (two 32-key score blocks) on bf16 MFMA, 32 on fp32 MFMA.
-    // The LDS footprint is kept under half a CU's LDS so that two workgroups
-    // share a CU and one's loads overlap the other's MFMA work.
     constexpr int KT = BF16 ? 64 : 32;
     constexpr int kKPitch = BF16 ? kHeadDim + 8 : kHeadDim + 4;
     constexpr int kVPitch = BF16 ? KT + 8 : KT + 4;
@@ -264,8 +275,8 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
     constexpr int kVBytes = kHeadDim * kVPitch * kElem;
     constexpr int kBlocks = KT / 32; // 32-key score blocks per tile
 
-    __shared__ __attribute__((aligned(16))) unsigned char k_lds[kKBytes];
-    __shared__ __attribute__((aligned(16))) unsigned char v_lds[kVBytes];
+    __shared__ __attribute__((aligned(16))) unsigned char k_lds[kBufs * kKBytes];
+    __shared__ __attribute__((aligned(16))) unsigned char v_lds[kBufs * kVBytes];
     // Dynamic LDS: the RoPE table (fused mode; its coordinates plus an
     // identity row), then the row table.
     extern __shared__ __attribute__((aligned(16))) unsigned char dyn_lds[];
@@ -384,8 +395,9 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
     constexpr int kKRows = KT / kRowsPerPass;       // K rows per thread
     constexpr int kVKeys = BF16 ? 2 : 1;            // keys per V word group
     constexpr int kVGroups = KT / kVKeys / kRowsPerPass; // V key groups per thread
-    static_assert(KT / kVKeys == 32, "32 V key groups per tile");
-    static_assert(kKRows * kRowsPerPass == KT && kVGroups * kRowsPerPass * kVKeys == KT, "staging split");
+    static_assert(kKRows >= 1 && kVGroups >= 1 && kKRows * kRowsPerPass == KT &&
+                      kVGroups * kRowsPerPass * kVKeys == KT,
+                  "staging split");
     const int kc = tid & 15;
     const int kr0 = tid >> 4;
     // RoPE of this thread's feature pairs 4kc .. 4kc+3: the coordinate of pair
@@ -411,11 +423,14 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
     };
     Stage st;
 
-    auto load_tile = [&](int tile) {
+    auto load_k_to = [&](int tile, uint32_t* dst) {
 #pragma unroll
         for (int j = 0; j < kKRows; j++)
             load_raw8(reinterpret_cast<const TIn*>(load_base + row_k[tile * KT + kr0 + kRowsPerPass * j]) + 8 * kc,
-                      st.k + j * kRW);
+                      dst + j * kRW);
+    };
+    auto load_k = [&](int tile) { load_k_to(tile, st.k); };
+    auto load_v = [&](int tile) {
 #pragma unroll
         for (int j = 0; j < kVGroups; j++)
 #pragma unroll
@@ -425,17 +440,20 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
                               8 * kc,
                           st.v + (j * kVKeys + i) * kRW);
     };
+    auto load_tile = [&](int tile) {
+        load_k(tile);
+        load_v(tile);
+    };
 
-    auto store_tile = [&](int tile) {
-        unsigned char* const kb = k_lds;
-        unsigned char* const vb = v_lds;
+    auto store_k_from = [&](int tile, int buf, const uint32_t* src) {
+        unsigned char* const kb = k_lds + buf * kKBytes;
 #pragma unroll
         for (int j = 0; j < kKRows; j++)
         {
             const int row = kr0 + kRowsPerPass * j;
             const int lds_row = (row & ~31) | key_permute(row & 31);
             float kv[8];
-            raw_to_float8<TIn>(st.k + j * kRW, kv);
+            raw_to_float8<TIn>(src + j * kRW, kv);
             if constexpr (FUSED)
             {
                 const uint32_t code = row_code[tile * KT + row];
@@ -463,6 +481,10 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
                 *reinterpret_cast<float4*>(ks + 4) = make_float4(kv[4], kv[5], kv[6], kv[7]);
             }
         }
+    };
+    auto store_k = [&](int tile, int buf) { store_k_from(tile, buf, st.k); };
+    auto store_v = [&](int buf) {
+        unsigned char* const vb = v_lds + buf * kVBytes;
         // V transposed: Vt[d][key], keys swizzled in groups of 8 per feature chunk.
 #pragma unroll
         for (int j = 0; j < kVGroups; j++)
@@ -496,11 +518,19 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
         }
         }
     };
+    auto store_tile = [&](int tile, int buf) {
+        store_k(tile, buf);
+        store_v(buf);
+    };
 
     // ---- prologue: tile 0's loads, the RoPE table into LDS (plus an
     // identity row after the last coordinate), Q rotated and scaled in
     // registers ----
     load_tile(0);
+    // The pipeline also stages K(1) before its first step.
+    uint32_t k1[PIPE ? kKRows * kRW : 1];
+    if constexpr (PIPE)
+        load_k_to(min(1, tiles - 1), k1);
     uint32_t q_code = 0; // RoPE coordinate word of this lane's query row
     if constexpr (FUSED)
     {
@@ -583,8 +613,7 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
     const int krow = col; // K rows are stored key-permuted
 
     // S^T = K Q^T of one tile: one 32x32 block per 32 keys; chains interleaved.
-    auto scores = [&](f32x16 (&s)[kBlocks]) {
-        constexpr int buf = 0;
+    auto scores = [&](f32x16 (&s)[kBlocks], int buf) {
 #pragma unroll
         for (int b = 0; b < kBlocks; b++)
 #pragma unroll
@@ -630,11 +659,14 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
         }
     };
 
-    // Online softmax of one tile's scores, then O^T += V^T P^T.
+    // Online softmax of one tile's scores; the probabilities replace them.
     // Register i of score block b holds key 32b + 16*(i/8) + 8*half + i%8.
-    auto softmax_pv = [&](f32x16 (&s)[kBlocks], int tile) {
-        constexpr int buf = 0;
-        if (tile == tiles - 1 && (L % KT))
+    // lazy: O is rescaled only when a row maximum grows by more than 2^8 (a
+    // wave-uniform branch); otherwise every tile rescales, without a branch,
+    // so that the code can be interleaved with independent MFMA work.
+    // may_mask: the tile can be the ragged last one.
+    auto softmax = [&](f32x16 (&s)[kBlocks], int tile, auto lazy, auto may_mask) {
+        if (decltype(may_mask)::value && tile == tiles - 1 && (L % KT))
         {
             const int key0 = tile * KT + 8 * half;
 #pragma unroll
@@ -651,7 +683,7 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
             for (int i = 0; i < 16; i++)
                 tile_max = fmaxf(tile_max, s[b][i]);
         tile_max = max_xor32(tile_max);
-        if (__any(tile_max > row_max + kRescaleThreshold))
+        if (!decltype(lazy)::value || __any(tile_max > row_max + kRescaleThreshold))
         {
             const float new_max = fmaxf(row_max, tile_max);
             const float alpha = __builtin_amdgcn_exp2f(row_max - new_max);
@@ -673,7 +705,10 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
                 psum += s[b][i];
             }
         row_sum += psum;
+    };
 
+    // O^T += V^T P^T of one tile.
+    auto pv = [&](const f32x16 (&s)[kBlocks], int buf) {
         if constexpr (BF16)
         {
             bf16x8 pb[2 * kBlocks];
@@ -736,21 +771,82 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
         }
     };
 
-    // Step t: stage tile t into LDS, refill the registers with tile t+1's
-    // loads, then scores, softmax and PV of tile t.
-    for (int tile = 0; tile < tiles; tile++)
+    using Yes = std::integral_constant<bool, true>;
+    using No = std::integral_constant<bool, false>;
+    if constexpr (PIPE)
     {
-        store_tile(tile);
+        // Software pipeline, one barrier per tile, K and V double-buffered
+        // (buffer t & 1 holds tile t). Step t:
+        //   1. S(t+1) = K(t+1) Q^T (MFMA) with the softmax of S(t) (VALU; fp32
+        //      rescales every tile, without a branch) and V(t+1) into its
+        //      buffer;
+        //   2. O += V(t) P(t) (MFMA) with K(t+2) into buffer t & 1.
+        // Buffer writes never meet reads of the same step: V(t+1)'s buffer
+        // was last read by step t-1's PV and K(t+2)'s by step t-1's scores.
+        // Register stages: V(t+1) and K(t+2) are loaded one step before they
+        // are stored; loads past the last tile are clamped to it (in bounds,
+        // never used).
+        const int last = tiles - 1;
+        store_tile(0, 0);
+        store_k_from(min(1, last), 1, k1);
+        load_v(min(1, last));
+        load_k(min(2, last));
         __syncthreads();
-        if (tile + 1 < tiles)
-            load_tile(tile + 1);
+        f32x16 s[kBlocks];
+        if (wave_active)
+            scores(s, 0);
+        __syncthreads(); // K buffer 0 is rewritten in step 0
+        for (int tile = 0; tile < last; tile++)
+        {
+            const int buf = tile & 1;
+            if (wave_active)
+            {
+                f32x16 sn[kBlocks];
+                scores(sn, buf ^ 1);
+                softmax(s, tile, std::integral_constant<bool, BF16>(), No());
+                store_v(buf ^ 1);
+                load_v(min(tile + 2, last));
+                pv(s, buf);
+                store_k(min(tile + 2, last), buf);
+                load_k(min(tile + 3, last));
+#pragma unroll
+                for (int b = 0; b < kBlocks; b++)
+                    s[b] = sn[b];
+            }
+            else
+            {
+                store_v(buf ^ 1);
+                load_v(min(tile + 2, last));
+                store_k(min(tile + 2, last), buf);
+                load_k(min(tile + 3, last));
+            }
+            __syncthreads();
+        }
         if (wave_active)
         {
-            f32x16 s[kBlocks];
-            scores(s);
-            softmax_pv(s, tile);
+            softmax(s, last, std::integral_constant<bool, BF16>(), Yes());
+            pv(s, last & 1);
         }
-        __syncthreads();
+    }
+    else
+    {
+        // Step t: stage tile t into LDS, refill the registers with tile t+1's
+        // loads, then scores, softmax and PV of tile t.
+        for (int tile = 0; tile < tiles; tile++)
+        {
+            store_tile(tile, 0);
+            __syncthreads();
+            if (tile + 1 < tiles)
+                load_tile(tile + 1);
+            if (wave_active)
+            {
+                f32x16 s[kBlocks];
+                scores(s, 0);
+                softmax(s, tile, Yes(), Yes());
+                pv(s, 0);
+            }
+            __syncthreads();
+        }
     }
 
     if (!q_valid)
@@ -784,33 +880,33 @@ __global__ __launch_bounds__(kThreads, 2) void window_attention_kernel(const Att
 
 } // namespace
 
-template <typename TIn, typename TOut, bool BF16, bool FUSED>
+template <typename TIn, typename TOut, bool BF16, bool FUSED, int VARIANT>
 static hipError_t launch_one(const AttentionLaunch& p, hipStream_t stream)
 {
     // RoPE table, then the row table: K and V row offsets and one coordinate
     // word per row, padded to whole 64-row tiles.
     const size_t row_table = static_cast<size_t>((p.max_window_tokens + 63) & ~63) * (2 * sizeof(long long) + 4);
     const size_t dynamic_lds = rope_table_bytes(FUSED, p.rope_coords) + row_table;
-    hipLaunchKernelGGL((window_attention_kernel<TIn, TOut, BF16, FUSED>), dim3(p.work_count), dim3(kThreads),
-                       dynamic_lds, stream, p);
+    hipLaunchKernelGGL((window_attention_kernel<TIn, TOut, BF16, FUSED, VARIANT>), dim3(p.work_count),
+                       dim3(VARIANT == kVariantWidePipe ? 512 : 256), dynamic_lds, stream, p);
     return hipGetLastError();
 }
 
-template <bool BF16, bool FUSED>
+template <bool BF16, bool FUSED, int VARIANT>
 static hipError_t launch_typed(const AttentionLaunch& p, hipStream_t stream)
 {
     const int in_size = FUSED ? p.video.elemsize : p.packed_in_elemsize;
     const int out_size = FUSED ? p.video_out.elemsize : 4;
     if (in_size == 4 && out_size == 4)
-        return launch_one<float, float, BF16, FUSED>(p, stream);
+        return launch_one<float, float, BF16, FUSED, VARIANT>(p, stream);
     if (in_size == 2 && out_size == 4)
-        return launch_one<uint16_t, float, BF16, FUSED>(p, stream);
+        return launch_one<uint16_t, float, BF16, FUSED, VARIANT>(p, stream);
     if constexpr (FUSED)
     {
         if (in_size == 4 && out_size == 2)
-            return launch_one<float, uint16_t, BF16, FUSED>(p, stream);
+            return launch_one<float, uint16_t, BF16, FUSED, VARIANT>(p, stream);
         if (in_size == 2 && out_size == 2)
-            return launch_one<uint16_t, uint16_t, BF16, FUSED>(p, stream);
+            return launch_one<uint16_t, uint16_t, BF16, FUSED, VARIANT>(p, stream);
     }
     return hipErrorInvalidValue;
 }
@@ -819,9 +915,19 @@ hipError_t launch_attention(const AttentionLaunch& p, hipStream_t stream)
 {
     if (p.work_count <= 0)
         return hipSuccess;
-    if (p.fused)
-        return p.bf16_mfma ? launch_typed<true, true>(p, stream) : launch_typed<false, true>(p, stream);
-    return p.bf16_mfma ? launch_typed<true, false>(p, stream) : launch_typed<false, false>(p, stream);
+    // Instantiated: bf16 MFMA in the narrow variant, fp32 MFMA in the 8-wave
+    // pipelined one.
+    if (p.bf16_mfma)
+    {
+        if (p.variant == kVariantNarrow)
+            return p.fused ? launch_typed<true, true, kVariantNarrow>(p, stream)
+                           : launch_typed<true, false, kVariantNarrow>(p, stream);
+        return hipErrorInvalidValue;
+    }
+    if (p.variant == kVariantWidePipe)
+        return p.fused ? launch_typed<false, true, kVariantWidePipe>(p, stream)
+                       : launch_typed<false, false, kVariantWidePipe>(p, stream);
+    return hipErrorInvalidValue;
 }
 
 } // namespace awa

@@ -160,14 +160,23 @@ int check_plan_uploaded(const awa_plan* plan)
 }
 
 // Work list of the attention kernel for `heads` heads: every (window, head)
-// unit is split into query blocks of kQueryRows rows; units are placed on the 8
+// unit is split into query blocks of rows_per_block rows; units are placed on the 8
 // XCDs by longest-processing-time first, and each XCD's items are laid out
 // at blockIdx = xcd + 8*j, since workgroups are dispatched round-robin over
 // the XCDs. All query blocks of one unit therefore share one XCD's L2 for
 // their K/V reads.
 constexpr int kXcds = 8;
 
-std::vector<awa::WorkItem> build_work(const awa_plan& plan, int heads)
+// Attention kernel variant per arithmetic: fp32 MFMA takes the 8-wave
+// pipeline (one workgroup per unit of up to 256 rows, its long MFMA tiles
+// hide the softmax and the staging), bf16 MFMA the 4-wave kernel (two
+// workgroups per CU).
+int attention_variant(bool bf16_mfma)
+{
+    return bf16_mfma ? awa::kVariantNarrow : awa::kVariantWidePipe;
+}
+
+std::vector<awa::WorkItem> build_work(const awa_plan& plan, int heads, int rows_per_block)
 {
     struct Unit
     {
@@ -178,7 +187,7 @@ std::vector<awa::WorkItem> build_work(const awa_plan& plan, int heads)
     for (size_t w = 0; w < plan.window_descs.size(); w++)
     {
         const int L = plan.window_descs[w].video_tokens + plan.text_tokens;
-        const int qblocks = (L + awa::kQueryRows - 1) / awa::kQueryRows;
+        const int qblocks = (L + rows_per_block - 1) / rows_per_block;
         for (int h = 0; h < heads; h++)
             units.push_back({static_cast<long long>(L) * L, static_cast<int>(w), h, qblocks});
     }
@@ -212,18 +221,24 @@ int ensure_workspace(const awa_plan& plan, int heads, size_t partial_bytes)
     std::lock_guard<std::mutex> lock(plan.mutex);
     if (plan.work_heads != heads || !plan.work)
     {
-        const std::vector<awa::WorkItem> work = build_work(plan, heads);
-        if (plan.work)
+        for (const bool wide : {false, true})
         {
-            (void)hipFree(plan.work);
-            plan.work = nullptr;
+            awa::WorkItem*& dst = wide ? plan.work_wide : plan.work;
+            int& count = wide ? plan.work_wide_count : plan.work_count;
+            const std::vector<awa::WorkItem> work =
+                build_work(plan, heads, wide ? awa::kWideQueryRows : awa::kQueryRows);
+            if (dst)
+            {
+                (void)hipFree(dst);
+                dst = nullptr;
+            }
+            if (hipMalloc(&dst, std::max<size_t>(work.size(), 1) * sizeof(awa::WorkItem)) != hipSuccess)
+                return fail(AWA_ERR_ALLOC, "work list allocation failed");
+            HIP_TRY(hipMemcpy(dst, work.data(), work.size() * sizeof(awa::WorkItem), hipMemcpyHostToDevice),
+                    "work list upload");
+            count = static_cast<int>(work.size());
         }
-        if (hipMalloc(&plan.work, std::max<size_t>(work.size(), 1) * sizeof(awa::WorkItem)) != hipSuccess)
-            return fail(AWA_ERR_ALLOC, "work list allocation failed");
-        HIP_TRY(hipMemcpy(plan.work, work.data(), work.size() * sizeof(awa::WorkItem), hipMemcpyHostToDevice),
-                "work list upload");
         plan.work_heads = heads;
-        plan.work_count = static_cast<int>(work.size());
     }
     if (partial_bytes > plan.text_partials_bytes)
     {
@@ -270,6 +285,8 @@ void free_device(awa_plan& plan)
     release(plan.dev.cu_seqlens);
     release(plan.dev.rope_cs);
     release(plan.work);
+    release(plan.work_wide);
+    plan.work_wide_count = 0;
     release(plan.text_partials);
     plan.text_partials_bytes = 0;
     plan.work_heads = 0;
@@ -651,8 +668,9 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
     p.video_out = sink;
     p.text_partials = plan->text_partials;
     p.windows = plan->dev.windows;
-    p.work = plan->work;
-    p.work_count = plan->work_count;
+    p.variant = attention_variant(p.bf16_mfma);
+    p.work = p.variant == awa::kVariantWidePipe ? plan->work_wide : plan->work;
+    p.work_count = p.variant == awa::kVariantWidePipe ? plan->work_wide_count : plan->work_count;
     p.rope_cs = plan->dev.rope_cs;
     p.rope_coords = plan->rope_coords;
     p.max_window_tokens = plan->max_window_tokens;
@@ -783,8 +801,10 @@ int awa_window_attention(const awa_plan* plan, const awa_blob* input, const awa_
     p.packed_out = static_cast<float*>(output->data);
     p.packed_out_row = output->cstep;
     p.windows = plan->dev.windows;
-    p.work = plan->work;
-    p.work_count = plan->work_count;
+    // Same variant choice as the fused layer, so that both give the same bits.
+    p.variant = attention_variant(p.bf16_mfma);
+    p.work = p.variant == awa::kVariantWidePipe ? plan->work_wide : plan->work;
+    p.work_count = p.variant == awa::kVariantWidePipe ? plan->work_wide_count : plan->work_count;
     p.max_window_tokens = plan->max_window_tokens;
     p.heads = heads;
     p.text_tokens = plan->text_tokens;

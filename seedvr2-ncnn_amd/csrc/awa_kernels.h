@@ -11,8 +11,12 @@ namespace awa
 
 constexpr int kHeadDim = 128;   // head_dim of the MFMA attention kernels
 constexpr int kRopeDim = 126;   // rope_dim of the fused kernel
-constexpr int kQueryWaves = 4;  // waves per attention workgroup, 32 query rows each
-constexpr int kQueryRows = 32 * kQueryWaves; // query rows per workgroup
+constexpr int kQueryRows = 128;     // query rows per workgroup (4 waves of 32)
+constexpr int kWideQueryRows = 256; // query rows per workgroup of the wide variant (8 waves)
+
+// Attention kernel variants.
+constexpr int kVariantNarrow = 0;   // 4 waves, single-buffered tiles
+constexpr int kVariantWidePipe = 1; // 8 waves, double-buffered, software-pipelined
 constexpr int kMaxRopeCoords = 128; // RoPE coordinates the fused kernel holds in LDS
 constexpr int kMaxFusedWindowTokens = 1536; // rows of the fused kernel's LDS row table
 
@@ -38,6 +42,7 @@ struct AttentionLaunch
 {
     bool fused;      // gather + RoPE from video/text sources, scatter to video/text
     bool bf16_mfma;  // AWA_COMPUTE_BF16
+    int variant;     // kVariant*: kVariantWidePipe takes work items of kWideQueryRows rows
     // fused inputs / outputs
     QkvSource video, text;
     VideoSink video_out;

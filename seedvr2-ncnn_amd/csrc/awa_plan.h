@@ -94,8 +94,10 @@ struct awa_plan
     // Lazily built per head count; guarded by mutex.
     mutable std::mutex mutex;
     mutable int work_heads = 0;
-    mutable awa::WorkItem* work = nullptr;
+    mutable awa::WorkItem* work = nullptr;      // query blocks of kQueryRows rows
     mutable int work_count = 0;
+    mutable awa::WorkItem* work_wide = nullptr; // query blocks of kWideQueryRows rows
+    mutable int work_wide_count = 0;
     mutable float* text_partials = nullptr;
     mutable size_t text_partials_bytes = 0;
 };
