@@ -866,9 +866,15 @@ __global__ __launch_bounds__(VARIANT == kVariantWidePipe ? 512 : 256,
         }
         else
         {
-            float* dst = p.text_partials +
-                         ((static_cast<long long>(item.window) * p.text_tokens + r.k) * p.heads + head) * kHeadDim;
-            store_row(dst, o, inv, half);
+            // Text partials are stored in the text output's type: with a bf16
+            // text output the per-window rows are rounded to bf16 before they
+            // are averaged, as the packed attention output is in a bf16 layer.
+            const long long off =
+                ((static_cast<long long>(item.window) * p.text_tokens + r.k) * p.heads + head) * kHeadDim;
+            if (p.text_partial_elemsize == 2)
+                store_row(static_cast<uint16_t*>(p.text_partials) + off, o, inv, half);
+            else
+                store_row(static_cast<float*>(p.text_partials) + off, o, inv, half);
         }
     }
     else

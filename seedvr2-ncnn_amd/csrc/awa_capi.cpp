@@ -667,6 +667,7 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
     p.text = {text_qkv->data, tl.token_stride, tl.qkv_stride, elem};
     p.video_out = sink;
     p.text_partials = plan->text_partials;
+    p.text_partial_elemsize = static_cast<int>(text_out->elemsize);
     p.windows = plan->dev.windows;
     p.variant = attention_variant(p.bf16_mfma);
     p.work = p.variant == awa::kVariantWidePipe ? plan->work_wide : plan->work;
@@ -682,7 +683,8 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
     HIP_TRY(awa::launch_attention(p, stream), "attention kernel launch");
     if (after_attention)
         HIP_TRY(hipEventRecord(after_attention, stream), "hipEventRecord");
-    HIP_TRY(awa::launch_text_mean(plan->text_partials, static_cast<int>(plan->windows.size()), plan->text_tokens,
+    HIP_TRY(awa::launch_text_mean(plan->text_partials, p.text_partial_elemsize, static_cast<int>(plan->windows.size()),
+                                  plan->text_tokens,
                                   vl.heads, vl.head_dim, text_out->data, text_out->cstep, text_out->elemsize, stream),
             "text mean kernel launch");
     return AWA_OK;

@@ -46,7 +46,8 @@ struct AttentionLaunch
     // fused inputs / outputs
     QkvSource video, text;
     VideoSink video_out;
-    float* text_partials; // [nwin][T_x][H][d] fp32
+    void* text_partials;  // [nwin][T_x][H][d], fp32 or bf16 (text_partial_elemsize)
+    int text_partial_elemsize;
     // packed inputs / outputs (fused == false)
     const void* packed_in;
     long long packed_in_row;
@@ -69,7 +70,7 @@ struct AttentionLaunch
 hipError_t launch_attention(const AttentionLaunch& p, hipStream_t stream);
 
 // text_out[k][head][:] = (sum_w partials[w][k][head][:]) / nwin, window order.
-hipError_t launch_text_mean(const float* partials, int window_count, int text_tokens, int heads, int head_dim,
+hipError_t launch_text_mean(const void* partials, int partial_elemsize, int window_count, int text_tokens, int heads, int head_dim,
                             void* text_out, long long text_token_stride, int out_elemsize, hipStream_t stream);
 
 // Generic (head_dim <= 1024) window attention over a packed [S][3H][d] blob;

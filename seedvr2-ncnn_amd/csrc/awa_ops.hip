@@ -151,10 +151,12 @@ __global__ void unpack_text_kernel(const int* text_positions, int window_count, 
     store_elem(out, k * out_row + e, out_elemsize, sum / static_cast<float>(window_count));
 }
 
-// ---- Fused-path text mean over the per-window partials [nwin][T_x][H][d] ----
+// ---- Fused-path text mean over the per-window partials [nwin][T_x][H][d]
+// (fp32 or bf16, the layer's output type) ----
 // One thread per output element pair; the window loop is unrolled so that 8
 // loads per thread are in flight, and the sum keeps window order.
-__global__ void text_mean_kernel(const float* partials, int window_count, int text_tokens, int row_elems,
+template <typename TPart>
+__global__ void text_mean_kernel(const TPart* partials, int window_count, int text_tokens, int row_elems,
                                  void* out, long long out_row, int out_elemsize)
 {
     const int pairs = row_elems / 2;
@@ -165,7 +167,17 @@ __global__ void text_mean_kernel(const float* partials, int window_count, int te
     const int k = static_cast<int>(idx / pairs);
     const int e = 2 * static_cast<int>(idx - static_cast<long long>(k) * pairs);
     const long long window_stride = static_cast<long long>(text_tokens) * row_elems;
-    const float* src = partials + static_cast<long long>(k) * row_elems + e;
+    const TPart* src = partials + static_cast<long long>(k) * row_elems + e;
+    // Element pair (x, y) of window w's partial row.
+    auto load_pair = [&](long long w) -> float2 {
+        if constexpr (sizeof(TPart) == 4)
+            return *reinterpret_cast<const float2*>(src + w * window_stride);
+        else
+        {
+            const uint32_t b = *reinterpret_cast<const uint32_t*>(src + w * window_stride);
+            return make_float2(__uint_as_float(b << 16), __uint_as_float(b & 0xffff0000u));
+        }
+    };
     float sx = 0.f, sy = 0.f;
     int w = 0;
     for (; w + 8 <= window_count; w += 8)
@@ -173,7 +185,7 @@ __global__ void text_mean_kernel(const float* partials, int window_count, int te
         float2 v[8];
 #pragma unroll
         for (int j = 0; j < 8; j++)
-            v[j] = *reinterpret_cast<const float2*>(src + (w + j) * window_stride);
+            v[j] = load_pair(w + j);
 #pragma unroll
         for (int j = 0; j < 8; j++)
         {
@@ -183,7 +195,7 @@ __global__ void text_mean_kernel(const float* partials, int window_count, int te
     }
     for (; w < window_count; w++)
     {
-        const float2 v = *reinterpret_cast<const float2*>(src + w * window_stride);
+        const float2 v = load_pair(w);
         sx += v.x;
         sy += v.y;
     }
@@ -319,13 +331,21 @@ unsigned grid_for(long long total)
 
 } // namespace
 
-hipError_t launch_text_mean(const float* partials, int window_count, int text_tokens, int heads, int head_dim,
+hipError_t launch_text_mean(const void* partials, int partial_elemsize, int window_count, int text_tokens, int heads, int head_dim,
                             void* text_out, long long text_token_stride, int out_elemsize, hipStream_t stream)
 {
     const int row_elems = heads * head_dim;
     const long long total = static_cast<long long>(text_tokens) * (row_elems / 2);
-    hipLaunchKernelGGL(text_mean_kernel, dim3(grid_for(total)), dim3(kBlock), 0, stream, partials, window_count,
-                       text_tokens, row_elems, text_out, text_token_stride, out_elemsize);
+    if (partial_elemsize == 4)
+        hipLaunchKernelGGL(text_mean_kernel<float>, dim3(grid_for(total)), dim3(kBlock), 0, stream,
+                           static_cast<const float*>(partials), window_count, text_tokens, row_elems, text_out,
+                           text_token_stride, out_elemsize);
+    else if (partial_elemsize == 2)
+        hipLaunchKernelGGL(text_mean_kernel<uint16_t>, dim3(grid_for(total)), dim3(kBlock), 0, stream,
+                           static_cast<const uint16_t*>(partials), window_count, text_tokens, row_elems, text_out,
+                           text_token_stride, out_elemsize);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

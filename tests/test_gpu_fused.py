@@ -11,7 +11,7 @@ import pytest
 import awa_hip as A
 import oracle as O
 from awa_cases import CONFIGS, HEAD_DIM, RAGGED, abs_err, geometry, qkv_inputs, rel_err
-from device_blobs import qkv_blob, read_mat3, read_video, video_out_blob, mat3
+from device_blobs import DeviceMat, mat3, qkv_blob, read_mat3, read_video, video_out_blob
 
 pytestmark = pytest.mark.gpu
 
@@ -19,14 +19,14 @@ FP32_ATOL = 1e-4
 BF16_RTOL = 2e-2
 
 
-def run_fused(g, video, text, compute, in_elem=4, out_elem=4, layout="a", batch_out=False):
+def run_fused(g, video, text, compute, in_elem=4, out_elem=4, layout="a", batch_out=False, text_out_elem=None):
     heads = video.shape[2]
     plan = A.Plan(A.LayerParams(*g.args, g.text_tokens, g.shifted))
     plan.upload()
     vq = qkv_blob(video, layout, in_elem)
     tq = qkv_blob(text, "a", in_elem)
     vo = video_out_blob(g.t, g.h, g.w, heads, HEAD_DIM, out_elem, batch_out)
-    to = mat3(HEAD_DIM, heads, g.text_tokens, out_elem)
+    to = mat3(HEAD_DIM, heads, g.text_tokens, out_elem if text_out_elem is None else text_out_elem)
     plan.forward(vq.blob, tq.blob, vo.blob, to.blob, compute)
     A.synchronize()
     return read_video(vo, g.t, g.h, g.w, heads, HEAD_DIM), read_mat3(to)
@@ -107,15 +107,44 @@ def test_layouts_identical(gpu, layout, batch_out):
     np.testing.assert_array_equal(got_t, base_t)
 
 
+def packed_attention_f32(g, video, text):
+    """Per-window attention rows [S][H][d] of the staged fp32 chain."""
+    heads = video.shape[2]
+    plan = A.Plan(A.LayerParams(*g.args, g.text_tokens, g.shifted))
+    plan.upload()
+    S = plan.info.sequence_tokens
+    vq = qkv_blob(video, "a", 4)
+    tq = qkv_blob(text, "a", 4)
+    packed = mat3(HEAD_DIM, 3 * heads, S, 4)
+    cu = DeviceMat(dict(w=plan.info.window_count + 1, dims=1), plan.info.window_count + 1, 4)
+    roped = mat3(HEAD_DIM, 3 * heads, S, 4)
+    att = mat3(HEAD_DIM, heads, S, 4)
+    plan.pack(vq.blob, tq.blob, packed.blob, cu.blob)
+    plan.mmrope(packed.blob, roped.blob)
+    plan.window_attention(roped.blob, att.blob, A.COMPUTE_F32)
+    A.synchronize()
+    return read_mat3(att)
+
+
 def test_bf16_output_rounding(gpu):
-    """bf16 outputs are the fp32 outputs rounded to nearest even."""
+    """bf16 video outputs are the fp32 outputs rounded to nearest even. A bf16
+    text output is the window-order mean of the per-window rows rounded to
+    bf16 (the packed attention output of a bf16 layer), itself rounded
+    (src/awa/awa_layers.cpp:768-775, src/awa/shader/awa_unpack.comp:47-58)."""
     g = geometry((1, 8, 8, 1, 2, 2, 4), True)
     print("case bf16 output rounding", flush=True)
-    video, text = qkv_inputs(g, 2, HEAD_DIM, 5)
+    heads = 2
+    video, text = qkv_inputs(g, heads, HEAD_DIM, 5)
     v32, t32 = run_fused(g, video, text, A.COMPUTE_F32, out_elem=4)
     v16, t16 = run_fused(g, video, text, A.COMPUTE_F32, out_elem=2)
     np.testing.assert_array_equal(v16, bf16_round(v32))
-    np.testing.assert_array_equal(t16, bf16_round(t32))
+    rows = packed_attention_f32(g, video, text)
+    _, t_expect = O.unpack_forward(g, bf16_round(rows), heads, HEAD_DIM)
+    np.testing.assert_array_equal(t16, bf16_round(t_expect))
+    # Mixed outputs: fp32 text keeps fp32 rows.
+    v16m, t32m = run_fused(g, video, text, A.COMPUTE_F32, out_elem=2, text_out_elem=4)
+    np.testing.assert_array_equal(v16m, v16)
+    np.testing.assert_array_equal(t32m, t32)
 
 
 # The benchmark workloads themselves: 33 frames 256x256 (9x16x16), 9 frames
