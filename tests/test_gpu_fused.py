@@ -187,3 +187,35 @@ def test_precision_combinations(gpu, in_elem, out_elem, compute):
         assert abs_err(got_v, ref_v) <= FP32_ATOL and abs_err(got_t, ref_t) <= FP32_ATOL
     else:
         assert rel_err(got_v, ref_v) <= BF16_RTOL and rel_err(got_t, ref_t) <= BF16_RTOL
+
+
+def test_text_mean_repeated_launches(gpu):
+    """The in-launch text mean leaves its counters ready for the next launch:
+    one plan run repeatedly, in both arithmetics and with the head count
+    changing between runs, gives the same bits every time."""
+    g = geometry(RAGGED[1], True)
+    print(f"case repeated launches {RAGGED[1]} shifted", flush=True)
+    plan = A.Plan(A.LayerParams(*g.args, g.text_tokens, g.shifted))
+    plan.upload()
+    first = {}
+    for heads in (2, 5, 2, 5):
+        video, text = qkv_inputs(g, heads, HEAD_DIM, 90 + heads)
+        vq = qkv_blob(video, "a", 4)
+        tq = qkv_blob(text, "a", 4)
+        for compute in (A.COMPUTE_F32, A.COMPUTE_BF16):
+            for _ in range(3):
+                vo = video_out_blob(g.t, g.h, g.w, heads, HEAD_DIM, 4, False)
+                to = mat3(HEAD_DIM, heads, g.text_tokens, 4)
+                plan.forward(vq.blob, tq.blob, vo.blob, to.blob, compute)
+                A.synchronize()
+                got_v = read_video(vo, g.t, g.h, g.w, heads, HEAD_DIM)
+                got_t = read_mat3(to)
+                key = (heads, compute)
+                if key not in first:
+                    ref_v, ref_t = O.awa_layer(g, video, text, heads, HEAD_DIM)
+                    tol = abs_err if compute == A.COMPUTE_F32 else rel_err
+                    bound = FP32_ATOL if compute == A.COMPUTE_F32 else BF16_RTOL
+                    assert tol(got_v, ref_v) <= bound and tol(got_t, ref_t) <= bound, key
+                    first[key] = (got_v, got_t)
+                np.testing.assert_array_equal(got_v, first[key][0])
+                np.testing.assert_array_equal(got_t, first[key][1])
