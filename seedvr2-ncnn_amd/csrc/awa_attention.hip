@@ -607,8 +607,17 @@ __global__ __launch_bounds__(VARIANT == kVariantWidePipe ? 512 : 256,
 #pragma unroll
         for (int i = 0; i < 16; i++)
             o[db][i] = 0.f;
-    float row_max = -INFINITY; // running maximum (log2 domain), possibly stale by < 2^8
-    float row_sum = 0.f;       // partial sum over this lane's keys
+    // The bf16 kernel keeps its scores relative to the running maximum: the
+    // score MFMA chains start from -row_max (negm), so that exp2 needs no
+    // subtraction. Before the first tile row_max is 0 and the first tile
+    // always sets it.
+    constexpr bool kRel = BF16 && !PIPE;
+    float row_max = kRel ? 0.f : -INFINITY; // running maximum (log2 domain), possibly stale by < 2^8
+    float row_sum = 0.f;                    // partial sum over this lane's keys
+    f32x16 negm;
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+        negm[i] = 0.f;
 
     const int krow = col; // K rows are stored key-permuted
 
@@ -619,6 +628,12 @@ __global__ __launch_bounds__(VARIANT == kVariantWidePipe ? 512 : 256,
 #pragma unroll
             for (int i = 0; i < 16; i++)
                 s[b][i] = 0.f;
+        if constexpr (kRel)
+        {
+#pragma unroll
+            for (int b = 0; b < kBlocks; b++)
+                s[b] = negm;
+        }
         if constexpr (BF16)
         {
             const uint16_t* ks =
@@ -683,6 +698,44 @@ __global__ __launch_bounds__(VARIANT == kVariantWidePipe ? 512 : 256,
             for (int i = 0; i < 16; i++)
                 tile_max = fmaxf(tile_max, s[b][i]);
         tile_max = max_xor32(tile_max);
+        if constexpr (kRel)
+        {
+            // tile_max is relative to row_max.
+            if (tile == 0 || __any(tile_max > kRescaleThreshold))
+            {
+                const float delta = tile == 0 ? tile_max : fmaxf(tile_max, 0.f);
+                if (tile != 0)
+                {
+                    const float alpha = __builtin_amdgcn_exp2f(-delta);
+                    row_sum *= alpha;
+#pragma unroll
+                    for (int db = 0; db < 4; db++)
+#pragma unroll
+                        for (int i = 0; i < 16; i++)
+                            o[db][i] *= alpha;
+                }
+                row_max += delta;
+#pragma unroll
+                for (int b = 0; b < kBlocks; b++)
+#pragma unroll
+                    for (int i = 0; i < 16; i++)
+                        s[b][i] -= delta;
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    negm[i] = -row_max;
+            }
+            float psum = 0.f;
+#pragma unroll
+            for (int b = 0; b < kBlocks; b++)
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                {
+                    s[b][i] = __builtin_amdgcn_exp2f(s[b][i]);
+                    psum += s[b][i];
+                }
+            row_sum += psum;
+            return;
+        }
         if (!decltype(lazy)::value || __any(tile_max > row_max + kRescaleThreshold))
         {
             const float new_max = fmaxf(row_max, tile_max);
