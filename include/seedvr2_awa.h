@@ -152,6 +152,38 @@ int awa_qkv_shape(const awa_blob* qkv, int tokens, int* heads, int* head_dim);
 int awa_forward(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv, const awa_blob* video_out,
                 const awa_blob* text_out, int compute, void* stream);
 
+/* The DiT block's q/k RMSNorm (affine, fp32 arithmetic and output): for every
+ * token and head, x * (1 / sqrt(mean(x^2 over head_dim) + eps)) * gamma, with
+ * separate gammas for video and text tokens (DitRMSNorm,
+ * src/dit/dit_precision.cpp:22-91 and src/dit/shader/dit_rmsnorm.comp;
+ * norm_q / norm_k of tools/reference/dit_block.py:258-263, :285-288).
+ * Gammas are device pointers to head_dim floats, 16-byte aligned. */
+typedef struct awa_qk_norm
+{
+    const float* q_video;
+    const float* k_video;
+    const float* q_text;
+    const float* k_text;
+    float eps; /* 1e-5 in the DiT */
+} awa_qk_norm;
+
+/* awa_forward with the DiT block's QKV prologue fused into the gather: the
+ * q/k RMSNorm above is applied to the Q and K rows as they are read, before
+ * MMRoPE, so video_qkv / text_qkv are the raw QKV projection outputs (fp32 or
+ * bf16). Replaces DitRMSNorm x 4 + DitQKVConcat (src/dit/dit_precision.cpp:95-142)
+ * + the AWA chain, which round-trip an fp32 [N][3H][d] QKV through memory
+ * (src/dit/dit_precision.cpp:314-315). Same blob rules as awa_forward. */
+int awa_forward_qknorm(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv,
+                       const awa_qk_norm* norm, const awa_blob* video_out, const awa_blob* text_out, int compute,
+                       void* stream);
+
+/* DitRMSNorm::forward (src/dit/dit_precision.cpp:63-86, dit_rmsnorm.comp): every
+ * row of width w = input.w of a dims-2/3 Mat (fp32 or bf16) normalised over w,
+ * times gamma[w] (device, fp32) when gamma is not null; output fp32 of the same
+ * shape. The sum of squares follows the shader's order (128 partial sums, then
+ * a pairwise tree), so results match the CPU oracle bit for bit. */
+int awa_rmsnorm(const awa_blob* input, const float* gamma, float eps, const awa_blob* output, void* stream);
+
 /* SeedVR2AWAPack (src/awa/awa_layers.cpp:419-458, :501-578): packed = Mat(d, 3H, S)
  * fp32, cu_seqlens = Mat(nwin+1) fp32. */
 int awa_pack(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv, const awa_blob* packed,

@@ -450,6 +450,44 @@ int orc_unpack_forward(const float* packed, const int* video_positions, int sour
 // fill_gaussian_noise (src/sampler/sampler.cpp:37-61): mt19937 seeded by
 // seed_seq{seed, stream_lo, stream_hi}, Box-Muller in double with midpoint
 // uniforms, cast to float; an odd count drops the last sine.
+// DitRMSNorm (src/dit/dit_precision.cpp:63-86) as its shader computes it
+// (src/dit/shader/dit_rmsnorm.comp:16-45): for each of `rows` rows of `width`
+// values, 128 partial sums (lane l adds x[i]^2 for i = l, l + 128, ...), a
+// pairwise reduction with stride 64, 32, ..., 1, coefficient =
+// inversesqrt(sum / width + eps), restated as 1 / sqrt(...) with correctly
+// rounded operations (the shader's inversesqrt is driver-defined to 2 ulp);
+// out = x * coefficient, then * gamma[i] when gamma is not null (affine).
+int orc_rmsnorm(const float* input, long long rows, int width, const float* gamma, float eps, float* output)
+{
+    if (rows < 0 || width <= 0)
+        return -1;
+    for (long long r = 0; r < rows; r++)
+    {
+        const float* x = input + r * width;
+        float sums[128];
+        for (int lane = 0; lane < 128; lane++)
+        {
+            float sum = 0.f;
+            for (int i = lane; i < width; i += 128)
+            {
+                const float square = x[i] * x[i];
+                sum = sum + square;
+            }
+            sums[lane] = sum;
+        }
+        for (int stride = 64; stride > 0; stride /= 2)
+            for (int lane = 0; lane < stride; lane++)
+                sums[lane] = sums[lane] + sums[lane + stride];
+        const float coefficient = 1.f / std::sqrt(sums[0] / static_cast<float>(width) + eps);
+        for (int i = 0; i < width; i++)
+        {
+            const float value = x[i] * coefficient;
+            output[r * width + i] = gamma ? value * gamma[i] : value;
+        }
+    }
+    return 0;
+}
+
 int orc_fill_gaussian(float* output, long long count, unsigned int seed, unsigned long long stream)
 {
     if (!output || count <= 0)

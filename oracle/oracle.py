@@ -45,6 +45,7 @@ def lib() -> ctypes.CDLL:
         _LIB.orc_seed_seq_words.argtypes = [ctypes.c_uint, ctypes.c_ulonglong, _p]
         _LIB.orc_round_bf16.argtypes = [_p, _p, _ll]
         _LIB.orc_awa_layer.argtypes = [_p, _p] + [_i] * 13 + [_p, _p]
+        _LIB.orc_rmsnorm.argtypes = [_p, _ll, _i, _p, ctypes.c_float, _p]
     return _LIB
 
 
@@ -205,6 +206,34 @@ def awa_layer(g: Geometry, video_qkv: np.ndarray, text_qkv: np.ndarray, heads: i
     if rc != 0:
         raise ValueError("oracle layer failed")
     return video, text
+
+
+def rmsnorm(x: np.ndarray, gamma, eps: float) -> np.ndarray:
+    """DitRMSNorm over the last axis (shader order); gamma None = no affine."""
+    x = np.ascontiguousarray(x, np.float32)
+    width = x.shape[-1]
+    out = np.zeros_like(x)
+    g = None if gamma is None else np.ascontiguousarray(gamma, np.float32)
+    if g is not None and g.shape != (width,):
+        raise ValueError("gamma must have the row width")
+    rc = lib().orc_rmsnorm(_ptr(x), x.size // width, width, None if g is None else _ptr(g), eps, _ptr(out))
+    if rc != 0:
+        raise ValueError("invalid rmsnorm arguments")
+    return out
+
+
+def qk_norm_inputs(video: np.ndarray, text: np.ndarray, gammas, eps: float):
+    """The DiT block's q/k RMSNorm on raw QKV: video [N][3][H][d], text
+    [T_x][3][H][d]; gammas (q_video, k_video, q_text, k_text) of head_dim each.
+    V passes through (tools/reference/dit_block.py:280-290)."""
+    q_video, k_video, q_text, k_text = gammas
+    v = np.array(video, np.float32, copy=True)
+    t = np.array(text, np.float32, copy=True)
+    v[:, 0] = rmsnorm(v[:, 0], q_video, eps)
+    v[:, 1] = rmsnorm(v[:, 1], k_video, eps)
+    t[:, 0] = rmsnorm(t[:, 0], q_text, eps)
+    t[:, 1] = rmsnorm(t[:, 1], k_text, eps)
+    return v, t
 
 
 def fill_gaussian(count: int, seed: int, stream: int = 0) -> np.ndarray:

@@ -34,10 +34,22 @@ EXPORTED_SYMBOLS = (
     "awa_event_synchronize", "awa_event_elapsed_ms", "awa_fill_normal", "awa_plan_create", "awa_plan_destroy",
     "awa_plan_info_get", "awa_plan_windows", "awa_plan_sequence_index", "awa_plan_cu_seqlens",
     "awa_plan_video_positions", "awa_plan_text_positions", "awa_plan_rope_table", "awa_plan_upload",
-    "awa_qkv_shape", "awa_forward", "awa_pack", "awa_mmrope", "awa_window_attention", "awa_unpack", "awa_cast",
+    "awa_qkv_shape", "awa_forward", "awa_forward_qknorm", "awa_rmsnorm", "awa_pack", "awa_mmrope",
+    "awa_window_attention", "awa_unpack", "awa_cast",
     "awa_stack_create", "awa_stack_destroy", "awa_stack_run", "awa_stack_set_profiling", "awa_stack_set_graph", "awa_stack_block_times",
     "awa_stack_block_flops",
 )
+
+
+class AwaQkNorm(ctypes.Structure):
+    """awa_qk_norm: device gamma pointers (q video, k video, q text, k text), eps."""
+    _fields_ = [
+        ("q_video", ctypes.c_void_p),
+        ("k_video", ctypes.c_void_p),
+        ("q_text", ctypes.c_void_p),
+        ("k_text", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+    ]
 
 
 class AwaBlob(ctypes.Structure):
@@ -113,6 +125,8 @@ def lib() -> ctypes.CDLL:
         L.awa_plan_upload.argtypes = [vp, vp]
         bp = ctypes.POINTER(AwaBlob)
         L.awa_forward.argtypes = [vp, bp, bp, bp, bp, i, vp]
+        L.awa_forward_qknorm.argtypes = [vp, bp, bp, ctypes.POINTER(AwaQkNorm), bp, bp, i, vp]
+        L.awa_rmsnorm.argtypes = [bp, vp, ctypes.c_float, bp, vp]
         L.awa_pack.argtypes = [vp, bp, bp, bp, bp, vp]
         L.awa_mmrope.argtypes = [vp, bp, bp, vp]
         L.awa_window_attention.argtypes = [vp, bp, bp, i, vp]
@@ -339,6 +353,12 @@ class Plan:
         check(lib().awa_forward(self.h, ctypes.byref(video_qkv), ctypes.byref(text_qkv), ctypes.byref(video_out),
                                 ctypes.byref(text_out), compute, _s(stream)), "awa_forward")
 
+    def forward_qknorm(self, video_qkv: AwaBlob, text_qkv: AwaBlob, norm: AwaQkNorm, video_out: AwaBlob,
+                       text_out: AwaBlob, compute: int = COMPUTE_F32, stream: Optional[Stream] = None) -> None:
+        check(lib().awa_forward_qknorm(self.h, ctypes.byref(video_qkv), ctypes.byref(text_qkv), ctypes.byref(norm),
+                                       ctypes.byref(video_out), ctypes.byref(text_out), compute, _s(stream)),
+              "awa_forward_qknorm")
+
     def pack(self, video_qkv: AwaBlob, text_qkv: AwaBlob, packed: AwaBlob, cu: AwaBlob,
              stream: Optional[Stream] = None) -> None:
         check(lib().awa_pack(self.h, ctypes.byref(video_qkv), ctypes.byref(text_qkv), ctypes.byref(packed),
@@ -401,6 +421,10 @@ class AttentionStack:
             self.destroy()
         except Exception:
             pass
+
+
+def rmsnorm(inp: AwaBlob, gamma_ptr: Optional[int], eps: float, out: AwaBlob, stream: Optional[Stream] = None) -> None:
+    check(lib().awa_rmsnorm(ctypes.byref(inp), gamma_ptr, eps, ctypes.byref(out), _s(stream)), "awa_rmsnorm")
 
 
 def cast(inp: AwaBlob, out: AwaBlob, stream: Optional[Stream] = None) -> None:

@@ -233,11 +233,27 @@ __device__ __forceinline__ float max_xor32(float x)
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Sum of x over each group of 16 consecutive lanes, in every lane of the
+// group (DPP: swap neighbours, swap pairs, mirror the quads of each half,
+// mirror the halves).
+__device__ __forceinline__ float sum16(float x)
+{
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xF, 0xF, false));
+    return x;
+}
+
 __device__ __forceinline__ float sum_xor32(float x)
 {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
+
+// Bytes of the dynamic-LDS K gammas of the fused q/k RMSNorm (video, text).
+template <bool NORM>
+constexpr int kNormLdsBytes = NORM ? 2 * kHeadDim * 4 : 0;
 
 // Bytes of the dynamic-LDS RoPE table: coords + 1 rows of 21 (cos, sin)
 // pairs, rounded up to 16 bytes.
@@ -254,10 +270,13 @@ __host__ __device__ inline int rope_table_bytes(bool fused, int rope_coords)
 //     software pipeline with one barrier per tile: the scores of tile t+1 and
 //     the PV of tile t are issued next to the softmax of tile t and the
 //     staging of the next tiles.
-template <typename TIn, typename TOut, bool BF16, bool FUSED, int VARIANT>
+// NORM (fused mode): the DiT block's q/k RMSNorm over head_dim is applied to
+// Q and K rows as they are gathered, before RoPE.
+template <typename TIn, typename TOut, bool BF16, bool FUSED, int VARIANT, bool NORM>
 __global__ __launch_bounds__(VARIANT == kVariantWidePipe ? 512 : 256,
                              VARIANT == kVariantWidePipe ? 1 : 2) void window_attention_kernel(const AttentionLaunch p)
 {
+    static_assert(!NORM || FUSED, "the q/k RMSNorm is fused into the gather");
     constexpr bool WIDE = VARIANT == kVariantWidePipe;
     constexpr bool PIPE = WIDE;
     constexpr int kThreads = WIDE ? 512 : 256;
@@ -280,8 +299,9 @@ __global__ __launch_bounds__(VARIANT == kVariantWidePipe ? 512 : 256,
     // Dynamic LDS: the RoPE table (fused mode; its coordinates plus an
     // identity row), then the row table.
     extern __shared__ __attribute__((aligned(16))) unsigned char dyn_lds[];
-    float* const rope_lds = reinterpret_cast<float*>(dyn_lds);
-    unsigned char* const row_dyn = dyn_lds + rope_table_bytes(FUSED, p.rope_coords);
+    float* const norm_lds = reinterpret_cast<float*>(dyn_lds); // NORM: K gammas, video then text
+    float* const rope_lds = reinterpret_cast<float*>(dyn_lds + kNormLdsBytes<NORM>);
+    unsigned char* const row_dyn = dyn_lds + kNormLdsBytes<NORM> + rope_table_bytes(FUSED, p.rope_coords);
 
     const WorkItem item = p.work[blockIdx.x];
     if (item.window < 0)
@@ -456,6 +476,24 @@ __global__ __launch_bounds__(VARIANT == kVariantWidePipe ? 512 : 256,
             raw_to_float8<TIn>(src + j * kRW, kv);
             if constexpr (FUSED)
             {
+                if constexpr (NORM)
+                {
+                    // RMSNorm of the K row over head_dim (its 16 chunks sit
+                    // in 16 consecutive lanes), then the video or text gamma.
+                    float ss = 0.f;
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        ss = fmaf(kv[e], kv[e], ss);
+                    const float coef = __builtin_amdgcn_rsqf(sum16(ss) * (1.f / kHeadDim) + p.norm_eps);
+                    const bool text = tile * KT + row >= win.video_tokens;
+                    const float* const g = norm_lds + (text ? kHeadDim : 0) + 8 * kc;
+                    const float4 g0 = *reinterpret_cast<const float4*>(g);
+                    const float4 g1 = *reinterpret_cast<const float4*>(g + 4);
+                    const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        kv[e] = (kv[e] * coef) * gv[e];
+                }
                 const uint32_t code = row_code[tile * KT + row];
 #pragma unroll
                 for (int q = 0; q < 4; q++)
@@ -545,6 +583,9 @@ __global__ __launch_bounds__(VARIANT == kVariantWidePipe ? 512 : 256,
         }
         if (tid < kRopeRow)
             rope_lds[n + tid] = (tid & 1) ? 0.f : 1.f;
+        if constexpr (NORM)
+            for (int i = tid; i < 2 * kHeadDim; i += kThreads)
+                norm_lds[i] = i < kHeadDim ? p.norm_gamma[1][i] : p.norm_gamma[3][i - kHeadDim];
         __syncthreads();
     }
 
@@ -553,11 +594,40 @@ __global__ __launch_bounds__(VARIANT == kVariantWidePipe ? 512 : 256,
     // fp32: lane holds features 64*half + [0,64).
     bf16x8 qb[BF16 ? 8 : 1];
     float qf[BF16 ? 1 : 64];
+    // Optional q RMSNorm over head_dim (the lane and its partner lane ^ 32
+    // hold the row's two halves): coefficient and the row's gamma.
+    float q_coef = 1.f;
+    const float* q_gamma = nullptr;
+    if constexpr (NORM)
+    {
+        float ss = 0.f;
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+        {
+            float v[8];
+            raw_to_float8<TIn>(qraw + c * kRW, v);
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                ss = fmaf(v[e], v[e], ss);
+        }
+        q_coef = __builtin_amdgcn_rsqf(sum_xor32(ss) * (1.f / kHeadDim) + p.norm_eps);
+        q_gamma = q_row >= win.video_tokens ? p.norm_gamma[2] : p.norm_gamma[0];
+    }
 #pragma unroll
     for (int c = 0; c < 8; c++)
     {
         float v[8];
         raw_to_float8<TIn>(qraw + c * kRW, v);
+        if constexpr (NORM)
+        {
+            const int f0 = BF16 ? 16 * c + 8 * half : 64 * half + 8 * c;
+            const float4 g0 = *reinterpret_cast<const float4*>(q_gamma + f0);
+            const float4 g1 = *reinterpret_cast<const float4*>(q_gamma + f0 + 4);
+            const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                v[e] = (v[e] * q_coef) * g[e];
+        }
         if constexpr (FUSED)
         {
             // 4 pairs from pair 8c + 4*half (bf16) or 32*half + 4c (fp32):
@@ -939,33 +1009,33 @@ __global__ __launch_bounds__(VARIANT == kVariantWidePipe ? 512 : 256,
 
 } // namespace
 
-template <typename TIn, typename TOut, bool BF16, bool FUSED, int VARIANT>
+template <typename TIn, typename TOut, bool BF16, bool FUSED, int VARIANT, bool NORM>
 static hipError_t launch_one(const AttentionLaunch& p, hipStream_t stream)
 {
     // RoPE table, then the row table: K and V row offsets and one coordinate
     // word per row, padded to whole 64-row tiles.
     const size_t row_table = static_cast<size_t>((p.max_window_tokens + 63) & ~63) * (2 * sizeof(long long) + 4);
-    const size_t dynamic_lds = rope_table_bytes(FUSED, p.rope_coords) + row_table;
-    hipLaunchKernelGGL((window_attention_kernel<TIn, TOut, BF16, FUSED, VARIANT>), dim3(p.work_count),
+    const size_t dynamic_lds = kNormLdsBytes<NORM> + rope_table_bytes(FUSED, p.rope_coords) + row_table;
+    hipLaunchKernelGGL((window_attention_kernel<TIn, TOut, BF16, FUSED, VARIANT, NORM>), dim3(p.work_count),
                        dim3(VARIANT == kVariantWidePipe ? 512 : 256), dynamic_lds, stream, p);
     return hipGetLastError();
 }
 
-template <bool BF16, bool FUSED, int VARIANT>
+template <bool BF16, bool FUSED, int VARIANT, bool NORM = false>
 static hipError_t launch_typed(const AttentionLaunch& p, hipStream_t stream)
 {
     const int in_size = FUSED ? p.video.elemsize : p.packed_in_elemsize;
     const int out_size = FUSED ? p.video_out.elemsize : 4;
     if (in_size == 4 && out_size == 4)
-        return launch_one<float, float, BF16, FUSED, VARIANT>(p, stream);
+        return launch_one<float, float, BF16, FUSED, VARIANT, NORM>(p, stream);
     if (in_size == 2 && out_size == 4)
-        return launch_one<uint16_t, float, BF16, FUSED, VARIANT>(p, stream);
+        return launch_one<uint16_t, float, BF16, FUSED, VARIANT, NORM>(p, stream);
     if constexpr (FUSED)
     {
         if (in_size == 4 && out_size == 2)
-            return launch_one<float, uint16_t, BF16, FUSED, VARIANT>(p, stream);
+            return launch_one<float, uint16_t, BF16, FUSED, VARIANT, NORM>(p, stream);
         if (in_size == 2 && out_size == 2)
-            return launch_one<uint16_t, uint16_t, BF16, FUSED, VARIANT>(p, stream);
+            return launch_one<uint16_t, uint16_t, BF16, FUSED, VARIANT, NORM>(p, stream);
     }
     return hipErrorInvalidValue;
 }
@@ -975,18 +1045,24 @@ hipError_t launch_attention(const AttentionLaunch& p, hipStream_t stream)
     if (p.work_count <= 0)
         return hipSuccess;
     // Instantiated: bf16 MFMA in the narrow variant, fp32 MFMA in the 8-wave
-    // pipelined one.
+    // pipelined one; the fused q/k RMSNorm in fused mode only.
+    if (p.qk_norm && !p.fused)
+        return hipErrorInvalidValue;
     if (p.bf16_mfma)
     {
-        if (p.variant == kVariantNarrow)
-            return p.fused ? launch_typed<true, true, kVariantNarrow>(p, stream)
-                           : launch_typed<true, false, kVariantNarrow>(p, stream);
-        return hipErrorInvalidValue;
+        if (p.variant != kVariantNarrow)
+            return hipErrorInvalidValue;
+        if (!p.fused)
+            return launch_typed<true, false, kVariantNarrow>(p, stream);
+        return p.qk_norm ? launch_typed<true, true, kVariantNarrow, true>(p, stream)
+                         : launch_typed<true, true, kVariantNarrow>(p, stream);
     }
-    if (p.variant == kVariantWidePipe)
-        return p.fused ? launch_typed<false, true, kVariantWidePipe>(p, stream)
-                       : launch_typed<false, false, kVariantWidePipe>(p, stream);
-    return hipErrorInvalidValue;
+    if (p.variant != kVariantWidePipe)
+        return hipErrorInvalidValue;
+    if (!p.fused)
+        return launch_typed<false, false, kVariantWidePipe>(p, stream);
+    return p.qk_norm ? launch_typed<false, true, kVariantWidePipe, true>(p, stream)
+                     : launch_typed<false, true, kVariantWidePipe>(p, stream);
 }
 
 } // namespace awa

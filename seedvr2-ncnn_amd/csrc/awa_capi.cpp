@@ -598,7 +598,18 @@ int awa_plan_upload(awa_plan* plan, void* stream)
 int awa_forward(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv, const awa_blob* video_out,
                 const awa_blob* text_out, int compute, void* stream)
 {
-    return awa::forward_fused(plan, video_qkv, text_qkv, video_out, text_out, compute, as_stream(stream), nullptr);
+    return awa::forward_fused(plan, video_qkv, text_qkv, nullptr, video_out, text_out, compute, as_stream(stream),
+                              nullptr);
+}
+
+int awa_forward_qknorm(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv,
+                       const awa_qk_norm* norm, const awa_blob* video_out, const awa_blob* text_out, int compute,
+                       void* stream)
+{
+    if (!norm)
+        return fail(AWA_ERR_INVALID, "null norm parameters");
+    return awa::forward_fused(plan, video_qkv, text_qkv, norm, video_out, text_out, compute, as_stream(stream),
+                              nullptr);
 }
 
 } // extern "C"
@@ -611,7 +622,7 @@ void set_error(const std::string& message)
     g_last_error = message;
 }
 
-int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv,
+int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv, const awa_qk_norm* norm,
                   const awa_blob* video_out, const awa_blob* text_out, int compute, hipStream_t stream,
                   hipEvent_t after_attention)
 {
@@ -655,6 +666,15 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
         !aligned16(text_out->data) || text_out->cstep % (16 / text_out->elemsize))
         return fail(AWA_ERR_INVALID, "output blobs must be 16-byte aligned with 16-byte aligned strides");
 
+    if (norm)
+    {
+        for (const float* g : {norm->q_video, norm->k_video, norm->q_text, norm->k_text})
+            if (!g || !aligned16(g))
+                return fail(AWA_ERR_INVALID, "norm gammas must be non-null and 16-byte aligned");
+        if (!(norm->eps >= 0.f) || !std::isfinite(norm->eps))
+            return fail(AWA_ERR_INVALID, "norm eps must be finite and non-negative");
+    }
+
     const size_t partial_bytes = plan->windows.size() * static_cast<size_t>(plan->text_tokens) * vl.heads *
                                  vl.head_dim * sizeof(float);
     if ((rc = ensure_workspace(*plan, vl.heads, partial_bytes)) != AWA_OK)
@@ -668,6 +688,15 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
     p.video_out = sink;
     p.text_partials = plan->text_partials;
     p.text_partial_elemsize = static_cast<int>(text_out->elemsize);
+    if (norm)
+    {
+        p.qk_norm = true;
+        p.norm_gamma[0] = norm->q_video;
+        p.norm_gamma[1] = norm->k_video;
+        p.norm_gamma[2] = norm->q_text;
+        p.norm_gamma[3] = norm->k_text;
+        p.norm_eps = norm->eps;
+    }
     p.windows = plan->dev.windows;
     p.variant = attention_variant(p.bf16_mfma);
     p.work = p.variant == awa::kVariantWidePipe ? plan->work_wide : plan->work;
@@ -847,6 +876,35 @@ int awa_unpack(const awa_plan* plan, const awa_blob* packed, const awa_blob* vid
                                     plan->text_tokens, packed->data, packed->cstep, packed->elemsize, text_out->data,
                                     text_out->cstep, text_out->elemsize, heads, head_dim, s),
             "unpack text kernel launch");
+    return AWA_OK;
+}
+
+int awa_rmsnorm(const awa_blob* input, const float* gamma, float eps, const awa_blob* output, void* stream)
+{
+    // DitRMSNorm::forward (src/dit/dit_precision.cpp:63-86): dims 2 or 3,
+    // elempack 1, no batch; the output keeps the shape, fp32 when affine,
+    // else the input's type.
+    if (!input || !output || !input->data || !output->data)
+        return fail(AWA_ERR_INVALID, "null blob");
+    if ((input->dims != 2 && input->dims != 3) || input->n != 1 || input->w <= 0 || input->h <= 0 ||
+        (input->dims == 3 && input->c <= 0) || (input->elemsize != 2 && input->elemsize != 4))
+        return fail(AWA_ERR_INVALID, "rmsnorm input must be a dims-2/3 fp32 or bf16 Mat");
+    if (output->dims != input->dims || output->w != input->w || output->h != input->h ||
+        (input->dims == 3 && output->c != input->c) || output->n != 1)
+        return fail(AWA_ERR_INVALID, "rmsnorm output must have the input's shape");
+    if (output->elemsize != (gamma ? 4 : input->elemsize))
+        return fail(AWA_ERR_INVALID, "rmsnorm output is fp32 with gamma, else the input's type");
+    if (!(eps >= 0.f) || !std::isfinite(eps))
+        return fail(AWA_ERR_INVALID, "eps must be finite and non-negative");
+    const int channels = input->dims == 3 ? input->c : 1;
+    const long long plane = static_cast<long long>(input->w) * input->h;
+    const long long in_cstep = input->dims == 3 ? input->cstep : plane;
+    const long long out_cstep = output->dims == 3 ? output->cstep : plane;
+    if (in_cstep < plane || out_cstep < plane)
+        return fail(AWA_ERR_INVALID, "channel step smaller than a channel");
+    HIP_TRY(awa::launch_rmsnorm(input->data, input->elemsize, in_cstep, output->data, output->elemsize, out_cstep,
+                                input->w, input->h, channels, gamma, eps, as_stream(stream)),
+            "rmsnorm kernel launch");
     return AWA_OK;
 }
 

@@ -14,9 +14,10 @@ namespace awa
 // Sets the calling thread's awa_last_error() text.
 void set_error(const std::string& message);
 
-// awa_forward with an optional event recorded between the attention kernel and
-// the text-mean kernel (for per-kernel timing).
-int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv,
+// awa_forward (norm null) or awa_forward_qknorm, with an optional event
+// recorded between the attention kernel and the text-mean kernel (for
+// per-kernel timing).
+int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv, const awa_qk_norm* norm,
                   const awa_blob* video_out, const awa_blob* text_out, int compute, hipStream_t stream,
                   hipEvent_t after_attention);
 

@@ -48,6 +48,10 @@ struct AttentionLaunch
     VideoSink video_out;
     void* text_partials;  // [nwin][T_x][H][d], fp32 or bf16 (text_partial_elemsize)
     int text_partial_elemsize;
+    // fused q/k RMSNorm over head_dim: gammas q video, k video, q text, k text
+    bool qk_norm;
+    const float* norm_gamma[4];
+    float norm_eps;
     // packed inputs / outputs (fused == false)
     const void* packed_in;
     long long packed_in_row;
@@ -104,6 +108,9 @@ struct CastShape
     int w, h, d, c, n;
     long long in_cstep, in_nstep, out_cstep, out_nstep;
 };
+hipError_t launch_rmsnorm(const void* in, int in_elemsize, long long in_cstep, void* out, int out_elemsize,
+                          long long out_cstep, int width, int rows, int channels, const float* gamma, float eps,
+                          hipStream_t stream);
 hipError_t launch_cast(const void* in, int in_elemsize, void* out, int out_elemsize, const CastShape& s,
                        hipStream_t stream);
 

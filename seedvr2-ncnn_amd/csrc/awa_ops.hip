@@ -208,6 +208,46 @@ __global__ void text_mean_kernel(const TPart* partials, int window_count, int te
             f32_to_bf16(sx / n) | (static_cast<uint32_t>(f32_to_bf16(sy / n)) << 16);
 }
 
+// ---- DitRMSNorm (src/dit/dit_precision.cpp:63-86, src/dit/shader/dit_rmsnorm.comp):
+// one 128-thread workgroup per (row, channel). Lane l sums x[i]^2 over i = l,
+// l + 128, ... (products and sums rounded separately, as the shader's
+// `precise` asks: no contraction here), the 128 partial sums are added
+// pairwise (stride 64, 32,
+// ..., 1), coefficient = 1 / sqrt(sum / width + eps); out = x * coefficient,
+// times gamma[i] when gamma is given. ----
+__global__ __launch_bounds__(128) void rmsnorm_kernel(const void* in, int in_elemsize, long long in_cstep, void* out,
+                                                      int out_elemsize, long long out_cstep, int width,
+                                                      const float* gamma, float eps)
+{
+#pragma clang fp contract(off)
+    __shared__ float sums[128];
+    const int lane = threadIdx.x;
+    const long long src = static_cast<long long>(blockIdx.y) * in_cstep + static_cast<long long>(blockIdx.x) * width;
+    const long long dst = static_cast<long long>(blockIdx.y) * out_cstep + static_cast<long long>(blockIdx.x) * width;
+    float sum = 0.f;
+    for (int i = lane; i < width; i += 128)
+    {
+        const float v = load_elem(in, src + i, in_elemsize);
+        sum += v * v;
+    }
+    sums[lane] = sum;
+    __syncthreads();
+    for (int stride = 64; stride > 0; stride /= 2)
+    {
+        if (lane < stride)
+            sums[lane] += sums[lane + stride];
+        __syncthreads();
+    }
+    const float coefficient = 1.f / sqrtf(sums[0] / static_cast<float>(width) + eps);
+    for (int i = lane; i < width; i += 128)
+    {
+        float v = load_elem(in, src + i, in_elemsize) * coefficient;
+        if (gamma)
+            v *= gamma[i];
+        store_elem(out, dst + i, out_elemsize, v);
+    }
+}
+
 // ---- Generic window attention, any head_dim: one wave per (window-row, head) ----
 // Lanes stride over features; online softmax over keys with wave reductions.
 __global__ void attention_generic_kernel(const void* packed_in, long long in_row, int in_elemsize, float* out,
@@ -418,6 +458,17 @@ hipError_t launch_cast(const void* in, int in_elemsize, void* out, int out_elems
     const long long total = static_cast<long long>(s.w) * s.h * s.d * s.c * s.n;
     hipLaunchKernelGGL(cast_kernel, dim3(grid_for(total)), dim3(kBlock), 0, stream, in, in_elemsize, out,
                        out_elemsize, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm(const void* in, int in_elemsize, long long in_cstep, void* out, int out_elemsize,
+                          long long out_cstep, int width, int rows, int channels, const float* gamma, float eps,
+                          hipStream_t stream)
+{
+    if (rows <= 0 || channels <= 0 || width <= 0)
+        return hipSuccess;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows, channels), dim3(128), 0, stream, in, in_elemsize, in_cstep, out,
+                       out_elemsize, out_cstep, width, gamma, eps);
     return hipGetLastError();
 }
 

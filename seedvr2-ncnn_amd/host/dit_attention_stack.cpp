@@ -202,7 +202,7 @@ int enqueue_step(awa_stack* stack, void* const* video_qkv, void* const* text_qkv
         const awa_blob tq = dense_mat3(text_qkv[b], D, 3 * H, info.text_tokens, elem);
         const awa_blob vo = dense_mat3(video_out[b], D, H, info.source_tokens, elem);
         const awa_blob to = dense_mat3(text_out[b], D, H, info.text_tokens, elem);
-        const int rc = awa::forward_fused(stack->plans[b & 1], &vq, &tq, &vo, &to,
+        const int rc = awa::forward_fused(stack->plans[b & 1], &vq, &tq, nullptr, &vo, &to,
                                           fp32 ? AWA_COMPUTE_F32 : AWA_COMPUTE_BF16, s, ev ? ev[1] : nullptr);
         if (rc != AWA_OK)
             return rc;

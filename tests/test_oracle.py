@@ -506,3 +506,71 @@ def test_round_bf16_matches_torch_rne():
     t = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     assert np.array_equal(O.round_bf16_bits(x), t)
     assert np.array_equal(awa_hip.f32_to_bf16_bits(x), t)
+
+
+# ---- DitRMSNorm restatement (src/dit/shader/dit_rmsnorm.comp) ----
+
+def _rms_f64(x, gamma, eps):
+    x = np.asarray(x, np.float64)
+    y = x / np.sqrt((x * x).mean(-1, keepdims=True) + eps)
+    return y if gamma is None else y * np.asarray(gamma, np.float64)
+
+
+@pytest.mark.parametrize("width", [128, 200, 2560])
+@pytest.mark.parametrize("affine", [False, True])
+def test_rmsnorm_matches_float64_definition(width, affine):
+    rng = np.random.RandomState(width + affine)
+    x = (rng.randn(33, width) * rng.uniform(0.01, 50, (33, 1))).astype(np.float32)
+    gamma = rng.uniform(-2, 2, width).astype(np.float32) if affine else None
+    got = O.rmsnorm(x, gamma, 1e-5)
+    ref = _rms_f64(x, gamma, 1e-5)
+    scale = np.abs(ref).max(-1, keepdims=True) + 1e-30
+    # Each output is a few fp32 roundings away from the exact value.
+    assert np.max(np.abs(got - ref) / scale) < 4e-6 * (1 + (gamma is not None))
+
+
+def test_rmsnorm_closed_forms():
+    eps = 1e-5
+    # A constant row c gives c / sqrt(c^2 + eps) times gamma.
+    for c in (0.0, 1.0, -3.5, 1e3):
+        x = np.full((1, 128), c, np.float32)
+        g = np.linspace(-1, 1, 128).astype(np.float32)
+        got = O.rmsnorm(x, g, eps)
+        want = (np.float64(c) / np.sqrt(np.float64(c) * c + eps)) * g.astype(np.float64)
+        assert np.allclose(got, want, rtol=1e-6, atol=1e-7), c
+    # With eps = 0 the norm is scale-invariant and the mean square of the
+    # output is 1.
+    x = np.random.RandomState(3).randn(7, 128).astype(np.float32)
+    a = O.rmsnorm(x, None, 0.0)
+    b = O.rmsnorm(np.float32(8.0) * x, None, 0.0)
+    assert np.array_equal(a, b)  # a power-of-two scale is exact
+    assert np.allclose((a.astype(np.float64) ** 2).mean(-1), 1.0, atol=1e-6)
+
+
+def test_rmsnorm_rejects_planted_mistakes():
+    """A sum instead of a mean, or eps outside the root, fails the float64 check."""
+    rng = np.random.RandomState(9)
+    x = rng.randn(4, 128).astype(np.float32)
+    ref = _rms_f64(x, None, 1e-5)
+    wrong_sum = x / np.sqrt((x.astype(np.float64) ** 2).sum(-1, keepdims=True) + 1e-5)
+    wrong_eps = x / (np.sqrt((x.astype(np.float64) ** 2).mean(-1, keepdims=True)) + 1e-5)
+    got = O.rmsnorm(x, None, 1e-5)
+    assert np.max(np.abs(got - ref)) < 1e-5
+    assert np.max(np.abs(wrong_sum - ref)) > 1e-2
+    x_small = (rng.randn(4, 128) * 1e-3).astype(np.float32)
+    ref_small = _rms_f64(x_small, None, 1e-5)
+    wrong_small = x_small / (np.sqrt((x_small.astype(np.float64) ** 2).mean(-1, keepdims=True)) + 1e-5)
+    assert np.max(np.abs(O.rmsnorm(x_small, None, 1e-5) - ref_small)) < 1e-5
+    assert np.max(np.abs(wrong_small - ref_small)) > 1e-2
+
+
+def test_qk_norm_inputs_normalises_q_and_k_only():
+    rng = np.random.RandomState(5)
+    video = rng.randn(6, 3, 2, 128).astype(np.float32)
+    text = rng.randn(3, 3, 2, 128).astype(np.float32)
+    gammas = [rng.uniform(0.5, 1.5, 128).astype(np.float32) for _ in range(4)]
+    v, t = O.qk_norm_inputs(video, text, gammas, 1e-5)
+    assert np.array_equal(v[:, 2], video[:, 2]) and np.array_equal(t[:, 2], text[:, 2])
+    for src, dst, gq, gk in ((video, v, gammas[0], gammas[1]), (text, t, gammas[2], gammas[3])):
+        assert np.allclose(dst[:, 0], _rms_f64(src[:, 0], gq, 1e-5), rtol=1e-5, atol=1e-6)
+        assert np.allclose(dst[:, 1], _rms_f64(src[:, 1], gk, 1e-5), rtol=1e-5, atol=1e-6)
