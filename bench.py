@@ -80,6 +80,64 @@ def cpu_baseline(sample_layers: int) -> dict:
     }
 
 
+def qk_prologue(A, bufs, stream, iters: int = 20) -> dict:
+    """The DiT block's QKV prologue at a bf16 block of the same workload (raw
+    bf16 QKV projection, bf16 MFMA, bf16 outputs): q/k RMSNorm fused into the
+    AWA gather (awa_forward_qknorm) against the reference's data flow, which
+    normalises Q and K into an fp32 QKV, promotes V to it and runs the layer
+    on that (DitRMSNorm x 4 + DitQKVConcat + AWA; here awa_rmsnorm x 4 +
+    awa_cast x 2 + awa_forward). ms per layer, HIP events over `iters` layers."""
+    t, h, w = GRID
+    N = t * h * w
+    row = HEADS * HEAD_DIM
+    gam = [A.DeviceBuffer(HEAD_DIM * 4) for _ in range(4)]
+    rng = np.random.RandomState(7)
+    for g in gam:
+        g.upload(rng.uniform(0.5, 1.5, HEAD_DIM).astype(np.float32))
+    norm = A.AwaQkNorm(*[g.ptr for g in gam], 1e-5)
+    raw = {"video": (bufs[0].ptr, N), "text": (bufs[1].ptr, TEXT)}
+    f32 = {k: A.DeviceBuffer(n * 3 * row * 4) for k, (_, n) in raw.items()}
+    vo, to = bufs[2].ptr, bufs[3].ptr
+    qkv = lambda ptr, n, es: A.mat(ptr, HEAD_DIM, 3 * HEADS, n, es)
+    part = lambda ptr, n, es, k: A.mat(ptr + k * row * es, HEAD_DIM, HEADS, n, es, cstep=3 * row)
+    out_v, out_t = A.mat(vo, HEAD_DIM, HEADS, N, 2), A.mat(to, HEAD_DIM, HEADS, TEXT, 2)
+    res = {}
+    for shifted in (False, True):
+        plan = A.Plan(A.LayerParams(t, h, w, *WINDOWS, TEXT, shifted))
+        plan.upload()
+
+        def fused():
+            plan.forward_qknorm(qkv(raw["video"][0], N, 2), qkv(raw["text"][0], TEXT, 2), norm, out_v, out_t,
+                                A.COMPUTE_BF16, stream)
+
+        def unfused():
+            for key, (gq, gk) in (("video", (gam[0], gam[1])), ("text", (gam[2], gam[3]))):
+                ptr, n = raw[key]
+                dst = f32[key].ptr
+                A.rmsnorm(part(ptr, n, 2, 0), gq.ptr, 1e-5, part(dst, n, 4, 0), stream)
+                A.rmsnorm(part(ptr, n, 2, 1), gk.ptr, 1e-5, part(dst, n, 4, 1), stream)
+                A.cast(part(ptr, n, 2, 2), part(dst, n, 4, 2), stream)
+            plan.forward(qkv(f32["video"].ptr, N, 4), qkv(f32["text"].ptr, TEXT, 4), out_v, out_t,
+                         A.COMPUTE_BF16, stream)
+
+        times = {}
+        for name, fn in (("fused_ms", fused), ("unfused_ms", unfused)):
+            for _ in range(3):
+                fn()
+            e0, e1 = A.Event(), A.Event()
+            e0.record(stream)
+            for _ in range(iters):
+                fn()
+            e1.record(stream)
+            stream.synchronize()
+            times[name] = round(e0.elapsed_ms(e1) / iters, 5)
+        times["speedup"] = round(times["unfused_ms"] / times["fused_ms"], 3)
+        res["shifted" if shifted else "unshifted"] = times
+        plan.destroy()
+    res["data"] = "bf16 raw QKV projection of a bf16 block, gammas U(0.5, 1.5), eps 1e-5"
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -243,6 +301,7 @@ def main() -> int:
             "avg_launch_ms": round(avg_ms, 5),
         },
     }
+    result["qk_prologue"] = qk_prologue(A, buffers[FP32_PREFIX], stream)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_sample_layers)
     print(json.dumps(result), flush=True)
