@@ -4,8 +4,14 @@
 // (:1237-1291); the device work is the C ABI's.
 #include "awa_layers.h"
 
+#include <cerrno>
+#include <cstdint>
 #include <cstdio>
+#include <cstdlib>
+#include <fstream>
 #include <limits>
+#include <sstream>
+#include <string>
 
 namespace seedvr2
 {
@@ -189,13 +195,116 @@ Mat Mat::external(const awa_blob& b)
 
 int ParamDict::get(int id, int default_value) const
 {
-    const auto it = values_.find(id);
-    return it == values_.end() ? default_value : it->second;
+    const auto it = ints_.find(id);
+    return it == ints_.end() ? default_value : it->second;
+}
+
+float ParamDict::get(int id, float default_value) const
+{
+    const auto f = floats_.find(id);
+    if (f != floats_.end())
+        return f->second;
+    const auto i = ints_.find(id);
+    return i == ints_.end() ? default_value : static_cast<float>(i->second);
 }
 
 void ParamDict::set(int id, int value)
 {
-    values_[id] = value;
+    ints_[id] = value;
+}
+
+void ParamDict::set(int id, float value)
+{
+    floats_[id] = value;
+}
+
+std::vector<float> ParamDict::get_array(int id) const
+{
+    const auto it = arrays_.find(id);
+    return it == arrays_.end() ? std::vector<float>() : it->second;
+}
+
+namespace
+{
+
+// Whole-string integer / float parse (no trailing characters).
+bool parse_int(const std::string& s, long long& out)
+{
+    if (s.empty())
+        return false;
+    char* end = nullptr;
+    errno = 0;
+    out = std::strtoll(s.c_str(), &end, 10);
+    return errno == 0 && end == s.c_str() + s.size();
+}
+
+bool parse_float(const std::string& s, float& out)
+{
+    if (s.empty())
+        return false;
+    char* end = nullptr;
+    errno = 0;
+    out = std::strtof(s.c_str(), &end);
+    return errno == 0 && end == s.c_str() + s.size();
+}
+
+bool is_float_text(const std::string& s)
+{
+    return s.find_first_of(".eE") != std::string::npos;
+}
+
+} // namespace
+
+int ParamDict::load_field(const std::string& field)
+{
+    const size_t eq = field.find('=');
+    long long key = 0;
+    if (eq == std::string::npos || !parse_int(field.substr(0, eq), key))
+        return -1;
+    const std::string value = field.substr(eq + 1);
+    if (key <= -23300)
+    {
+        // Array: -23300 - id = count,v1,...,vcount.
+        const int id = static_cast<int>(-23300 - key);
+        std::vector<std::string> parts;
+        size_t start = 0;
+        while (true)
+        {
+            const size_t comma = value.find(',', start);
+            parts.push_back(value.substr(start, comma == std::string::npos ? std::string::npos : comma - start));
+            if (comma == std::string::npos)
+                break;
+            start = comma + 1;
+        }
+        long long count = 0;
+        if (!parse_int(parts[0], count) || count < 0 || static_cast<size_t>(count) + 1 != parts.size())
+            return -1;
+        std::vector<float> values;
+        for (size_t i = 1; i < parts.size(); i++)
+        {
+            float v = 0.f;
+            if (!parse_float(parts[i], v))
+                return -1;
+            values.push_back(v);
+        }
+        arrays_[id] = values;
+        return 0;
+    }
+    if (key < 0 || key > 0x7fffffff)
+        return -1;
+    if (is_float_text(value))
+    {
+        float v = 0.f;
+        if (!parse_float(value, v))
+            return -1;
+        floats_[static_cast<int>(key)] = v;
+        return 0;
+    }
+    long long v = 0;
+    if (!parse_int(value, v) || v < INT32_MIN || v > INT32_MAX)
+        return -1;
+    ints_[static_cast<int>(key)] = static_cast<int>(v);
+    return 0;
 }
 
 int Layer::load_param(const ParamDict&)
@@ -245,6 +354,95 @@ std::vector<std::string> Net::custom_layer_types() const
     for (const auto& kv : registry_)
         types.push_back(kv.first);
     return types;
+}
+
+int Net::load_param(const char* path)
+{
+    std::ifstream in(path ? path : "");
+    if (!in)
+    {
+        error_ = std::string("cannot open ") + (path ? path : "(null)");
+        return -1;
+    }
+    std::stringstream text;
+    text << in.rdbuf();
+    return load_param_mem(text.str().c_str());
+}
+
+int Net::load_param_mem(const char* text)
+{
+    layers_.clear();
+    blob_count_ = 0;
+    auto fail_load = [&](const std::string& message) {
+        layers_.clear();
+        blob_count_ = 0;
+        error_ = message;
+        return -1;
+    };
+    if (!text)
+        return fail_load("null text");
+    std::istringstream lines(text);
+    std::string line;
+    if (!std::getline(lines, line) || line.substr(0, line.find_first_of(" \t\r")) != "7767517")
+        return fail_load("not an ncnn param file (magic 7767517 expected)");
+    long long layer_count = 0, blob_count = 0;
+    {
+        if (!std::getline(lines, line))
+            return fail_load("missing layer and blob counts");
+        std::istringstream counts(line);
+        std::string a, b, extra;
+        if (!(counts >> a >> b) || (counts >> extra) || !parse_int(a, layer_count) || !parse_int(b, blob_count) ||
+            layer_count <= 0 || blob_count <= 0)
+            return fail_load("invalid layer and blob counts: " + line);
+    }
+    std::map<std::string, int> produced;
+    while (std::getline(lines, line))
+    {
+        std::istringstream fields(line);
+        std::vector<std::string> f;
+        for (std::string tok; fields >> tok;)
+            f.push_back(tok);
+        if (f.empty())
+            continue;
+        long long nb = 0, nt = 0;
+        if (f.size() < 4 || !parse_int(f[2], nb) || !parse_int(f[3], nt) || nb < 0 || nt < 0 ||
+            f.size() < 4 + static_cast<size_t>(nb + nt))
+            return fail_load("invalid layer line: " + line);
+        ParamLayer l;
+        l.type = f[0];
+        l.name = f[1];
+        l.bottoms.assign(f.begin() + 4, f.begin() + 4 + nb);
+        l.tops.assign(f.begin() + 4 + nb, f.begin() + 4 + nb + nt);
+        for (size_t i = 4 + nb + nt; i < f.size(); i++)
+            if (l.pd.load_field(f[i]) != 0)
+                return fail_load("invalid parameter " + f[i] + " in layer " + l.name);
+        for (const std::string& top : l.tops)
+            if (!produced.emplace(top, 1).second)
+                return fail_load("blob " + top + " produced twice");
+        if (registry_.count(l.type))
+        {
+            l.layer = create_custom_layer(l.type.c_str());
+            if (!l.layer || l.layer->load_param(l.pd) != 0)
+                return fail_load("load_param failed for layer " + l.name + " (" + l.type + ")");
+        }
+        layers_.push_back(std::move(l));
+    }
+    if (static_cast<long long>(layers_.size()) != layer_count)
+        return fail_load("layer count " + std::to_string(layer_count) + " but " + std::to_string(layers_.size()) +
+                         " layer lines");
+    if (static_cast<long long>(produced.size()) > blob_count)
+        return fail_load("more blobs produced than the declared blob count");
+    blob_count_ = static_cast<int>(blob_count);
+    error_.clear();
+    return 0;
+}
+
+const ParamLayer* Net::find_layer(const std::string& name) const
+{
+    for (const ParamLayer& l : layers_)
+        if (l.name == name)
+            return &l;
+    return nullptr;
 }
 
 } // namespace hip

@@ -96,15 +96,25 @@ private:
     int allocate(Allocator* allocator);
 };
 
-// Integer parameters by id (ncnn::ParamDict::get / set for int values).
+// Parameters by id (ncnn::ParamDict::get / set): integers, floats and
+// arrays, as a .param line gives them (`id=int`, `id=float`,
+// `-23300-id=n,v1,...,vn`).
 class ParamDict
 {
 public:
     int get(int id, int default_value) const;
+    float get(int id, float default_value) const;
     void set(int id, int value);
+    void set(int id, float value);
+    // Array parameter id, empty when absent.
+    std::vector<float> get_array(int id) const;
+    // Parses one `key=value` field of a .param layer line; -1 when malformed.
+    int load_field(const std::string& field);
 
 private:
-    std::map<int, int> values_;
+    std::map<int, int> ints_;
+    std::map<int, float> floats_;
+    std::map<int, std::vector<float>> arrays_;
 };
 
 // The ncnn::Option fields the AWA layers read, plus the HIP stream.
@@ -137,7 +147,22 @@ public:
 typedef Layer* (*layer_creator_func)(void* userdata);
 typedef void (*layer_destroyer_func)(Layer* layer, void* userdata);
 
-// Custom-layer registry with ncnn::Net's register_custom_layer signature.
+// One layer line of an ncnn .param file.
+struct ParamLayer
+{
+    std::string type, name;
+    std::vector<std::string> bottoms, tops;
+    ParamDict pd;
+    std::unique_ptr<Layer> layer; // registered types only; other types are recorded, not run
+};
+
+// Custom-layer registry with ncnn::Net's register_custom_layer signature, and
+// ncnn::Net::load_param for the .param text format the reference's packages
+// use (magic 7767517, "layer_count blob_count", then one line per layer:
+// type name bottom_count top_count bottoms... tops... params...;
+// tools/export_dit_block.py:38-124, :578-644; read by load_graph,
+// src/dit/dit_stack.cpp:167-220). Layers of registered types are created and
+// given their ParamDict; a layer's load_param failure fails the load.
 class Net
 {
 public:
@@ -147,6 +172,14 @@ public:
     std::unique_ptr<Layer> create_custom_layer(const char* type) const;
     std::vector<std::string> custom_layer_types() const;
 
+    // 0, or -1 with the message in last_error() (the net is left empty).
+    int load_param(const char* path);
+    int load_param_mem(const char* text);
+    const std::vector<ParamLayer>& layers() const { return layers_; }
+    const ParamLayer* find_layer(const std::string& name) const;
+    int blob_count() const { return blob_count_; }
+    const std::string& last_error() const { return error_; }
+
 private:
     struct Entry
     {
@@ -154,6 +187,9 @@ private:
         void* userdata;
     };
     std::map<std::string, Entry> registry_;
+    std::vector<ParamLayer> layers_;
+    int blob_count_ = 0;
+    std::string error_;
 };
 
 } // namespace hip

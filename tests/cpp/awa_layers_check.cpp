@@ -4,6 +4,10 @@
 //
 //   awa_layers_check params
 //       Host-only checks of registration, params, runtime spec and windows.
+//   awa_layers_check param
+//       Host-only checks of .param loading: a DiT block's AWA lines in the
+//       reference export's format, static and dynamic (-1) grids, and
+//       malformed files.
 //   awa_layers_check forward OUTDIR t h w nt nh nw text shifted heads bf16
 //       Seeded inputs on device 0, the four-layer chain and the fused chain;
 //       writes inputs and outputs as float32 files into OUTDIR and prints the
@@ -89,6 +93,98 @@ int run_params()
            "make_awa_windows 2x16x16 shifted");
     expect(seedvr2::make_awa_windows(0, 16, 16, 1, 8, 8, false).empty(), "make_awa_windows invalid");
     std::printf("%s\n", failures ? "params: FAILED" : "params: all passed");
+    return failures ? 1 : 0;
+}
+
+// A DiT block's AWA section as the reference's export writes it
+// (tools/export_dit_block.py:578-604, :639-644, :740-743): Pack, MMRoPE,
+// WindowAttention, Unpack, the video batch reshape, and a consumer Gemm.
+std::string block_param(const char* t, const char* h, const char* w, int shifted)
+{
+    const std::string grid = std::string("0=") + t + " 1=" + h + " 2=" + w;
+    const std::string rest = " 3=3 4=8 5=8 6=64 7=" + std::to_string(shifted);
+    return "7767517\n"
+           "8 10\n"
+           "Input in0 0 1 vid_qkv 0=128 1=60 2=2304\n"
+           "Input in1 0 1 txt_qkv 0=128 1=60 2=64\n"
+           "SeedVR2AWAPack awa_pack 2 2 vid_qkv txt_qkv packed awa_cu_seqlens " + grid + rest + "\n"
+           "SeedVR2MMRoPE mmrope 1 1 packed roped " + grid + rest + " 8=126\n"
+           "SeedVR2WindowAttention awa_attention 1 1 roped attended " + grid + rest + "\n"
+           "SeedVR2AWAUnpack awa_unpack 1 2 attended vid_out txt_out " + grid + rest + "\n"
+           "Reshape reshape_awa_video_batch 1 1 vid_out awa_video_batch 0=2560 1=-1\n"
+           "Gemm gemm_0 1 1 awa_video_batch proj 10=-1 2=0 3=1 4=0 5=1 6=1 7=0 8=2560 9=2560 -23310=3,1.0,0.5,-2\n";
+}
+
+int run_param()
+{
+    for (const int shifted : {0, 1})
+    {
+        Net net;
+        register_seedvr2_awa_layers(net);
+        const std::string text = block_param("9", "16", "16", shifted);
+        expect(net.load_param_mem(text.c_str()) == 0, "static 9x16x16 block loads");
+        expect(net.layers().size() == 8 && net.blob_count() == 10, "8 layers, 10 blobs");
+        const char* awa[4] = {"awa_pack", "mmrope", "awa_attention", "awa_unpack"};
+        for (const char* name : awa)
+        {
+            const auto* l = net.find_layer(name);
+            const auto* base = l && l->layer ? static_cast<const SeedVR2AwaLayerBase*>(l->layer.get()) : nullptr;
+            awa_plan_info info{};
+            expect(base && awa_plan_info_get(base->plan(), &info) == 0 && info.source_tokens == 2304 &&
+                       info.window_count == (shifted ? 36 : 12) && info.sequence_tokens == (shifted ? 4608 : 3072),
+                   name);
+        }
+        const auto* unpack = net.find_layer("awa_unpack");
+        expect(unpack && unpack->bottoms.size() == 1 && unpack->tops.size() == 2 && unpack->tops[0] == "vid_out",
+               "unpack blobs");
+        const auto* reshape = net.find_layer("reshape_awa_video_batch");
+        expect(reshape && !reshape->layer && reshape->bottoms[0] == "vid_out" && reshape->pd.get(1, 0) == -1,
+               "video batch reshape recorded, height -1");
+        const auto* gemm = net.find_layer("gemm_0");
+        const std::vector<float> arr = gemm ? gemm->pd.get_array(10) : std::vector<float>();
+        expect(gemm && arr.size() == 3 && arr[1] == 0.5f && arr[2] == -2.f && gemm->pd.get(8, 0) == 2560,
+               "foreign layer params, array field");
+    }
+    // The dynamic package template: 0=-1 1=-1 2=-1 takes the session grid.
+    seedvr2::AwaRuntimeSpec spec{9, 32, 32, 9 * 32 * 32};
+    Net dyn;
+    register_seedvr2_awa_layers(dyn, &spec);
+    const std::string dyn_text = block_param("-1", "-1", "-1", 1);
+    expect(dyn.load_param_mem(dyn_text.c_str()) == 0, "dynamic block loads with a runtime spec");
+    {
+        const auto* l = dyn.find_layer("awa_attention");
+        awa_plan_info info{};
+        expect(l && l->layer &&
+                   awa_plan_info_get(static_cast<const SeedVR2AwaLayerBase*>(l->layer.get())->plan(), &info) == 0 &&
+                   info.source_tokens == 9216 && info.window_count == 100,
+               "dynamic grid 9x32x32 shifted: 100 windows");
+    }
+    Net nospec;
+    register_seedvr2_awa_layers(nospec);
+    expect(nospec.load_param_mem(dyn_text.c_str()) == -1 && nospec.layers().empty(),
+           "dynamic block without a runtime spec fails");
+    // Malformed files.
+    Net bad;
+    register_seedvr2_awa_layers(bad);
+    std::string t = block_param("9", "16", "16", 0);
+    expect(bad.load_param_mem(("123\n" + t.substr(t.find('\n') + 1)).c_str()) == -1, "bad magic");
+    std::string wrong_count = t;
+    wrong_count.replace(wrong_count.find("8 10"), 4, "9 10");
+    expect(bad.load_param_mem(wrong_count.c_str()) == -1, "layer count mismatch");
+    std::string short_line = t + "Split s 1\n";
+    expect(bad.load_param_mem(short_line.c_str()) == -1, "truncated layer line");
+    std::string bad_param = t;
+    bad_param.replace(bad_param.find("7=0\nSeedVR2MMRoPE"), 3, "7=x");
+    expect(bad.load_param_mem(bad_param.c_str()) == -1, "non-numeric parameter");
+    std::string zero_windows = t;
+    zero_windows.replace(zero_windows.find("3=3 4=8 5=8 6=64 7=0\nSeedVR2AWAUnpack") , 3, "3=0");
+    expect(bad.load_param_mem(zero_windows.c_str()) == -1 && !bad.last_error().empty(),
+           "layer load_param failure fails the load");
+    std::string dup = t;
+    dup.replace(dup.find("packed roped"), 12, "packed packed");
+    expect(bad.load_param_mem(dup.c_str()) == -1, "blob produced twice");
+    expect(bad.load_param("/nonexistent/dit_block_00.ncnn.param") == -1, "missing file");
+    std::printf("%s\n", failures ? "param: FAILED" : "param: all passed");
     return failures ? 1 : 0;
 }
 
@@ -219,6 +315,9 @@ int main(int argc, char** argv)
         return run_params();
     if (argc >= 2 && std::strcmp(argv[1], "forward") == 0)
         return run_forward(argc, argv);
-    std::fprintf(stderr, "usage: %s params | forward OUTDIR t h w nt nh nw text shifted heads bf16\n", argv[0]);
+    if (argc >= 2 && std::strcmp(argv[1], "param") == 0)
+        return run_param();
+    std::fprintf(stderr, "usage: %s params | param | forward OUTDIR t h w nt nh nw text shifted heads bf16\n",
+                 argv[0]);
     return 2;
 }

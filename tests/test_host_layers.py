@@ -31,6 +31,16 @@ def test_layer_params_and_registration():
     assert "params: all passed" in r.stdout
 
 
+def test_param_file_loading():
+    """ncnn .param text with a DiT block's AWA lines in the reference export's
+    format (tools/export_dit_block.py:578-644): static and dynamic grids, the
+    video batch reshape, foreign layers with array params, malformed files."""
+    r = run_check("param")
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "param: all passed" in r.stdout
+
+
 FORWARD_CASES = [
     # t, h, w, nt, nh, nw, text, shifted, heads, bf16
     ((1, 16, 16, 1, 8, 8, 64, 0), 4, 0),
