@@ -698,14 +698,16 @@ __global__ __launch_bounds__(VARIANT == kVariantWidePipe ? 512 : 256,
 #pragma unroll
             for (int i = 0; i < 16; i++)
                 s[b][i] = 0.f;
-        if constexpr (kRel)
-        {
-#pragma unroll
-            for (int b = 0; b < kBlocks; b++)
-                s[b] = negm;
-        }
         if constexpr (BF16)
         {
+            // The chains start from -row_max in the relative form (the first
+            // MFMA's C operand), from zero otherwise.
+            f32x16 c0;
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                c0[i] = 0.f;
+            if constexpr (kRel)
+                c0 = negm;
             const uint16_t* ks =
                 reinterpret_cast<const uint16_t*>(k_lds + buf * kKBytes) + krow * kKPitch + 8 * half;
             bf16x8 ka[kBlocks][8];
@@ -715,7 +717,10 @@ __global__ __launch_bounds__(VARIANT == kVariantWidePipe ? 512 : 256,
                 for (int b = 0; b < kBlocks; b++)
                     ka[b][c] = *reinterpret_cast<const bf16x8*>(ks + b * 32 * kKPitch + 16 * c);
 #pragma unroll
-            for (int c = 0; c < 8; c++)
+            for (int b = 0; b < kBlocks; b++)
+                s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[b][0], qb[0], c0, 0, 0, 0);
+#pragma unroll
+            for (int c = 1; c < 8; c++)
 #pragma unroll
                 for (int b = 0; b < kBlocks; b++)
                     s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[b][c], qb[c], s[b], 0, 0, 0);
@@ -844,19 +849,20 @@ __global__ __launch_bounds__(VARIANT == kVariantWidePipe ? 512 : 256,
                     pb[2 * b + 1][e] = static_cast<__bf16>(s[b][8 + e]);
                 }
             // The four output chains are interleaved: consecutive MFMAs are
-            // independent.
-            const uint16_t* vt = reinterpret_cast<const uint16_t*>(v_lds + buf * kVBytes);
+            // independent. With d = 32 db + col (col < 32), 8 vt_swizzle(d)
+            // = 16 db + 8 (col / 16), so the swizzled column (8 half + 16 j)
+            // ^ 8 vt_swizzle(d) is a lane term, 8 (half ^ col / 16), plus
+            // (16 j) ^ (16 db): one lane base plus an immediate per read.
+            static_assert(KT == 64, "swizzle split for 64-key tiles");
+            const uint16_t* vt = reinterpret_cast<const uint16_t*>(v_lds + buf * kVBytes) + col * kVPitch +
+                                 8 * (half ^ (col >> 4));
 #pragma unroll
             for (int j = 0; j < 2 * kBlocks; j++)
             {
                 bf16x8 va[4];
 #pragma unroll
                 for (int db = 0; db < 4; db++)
-                {
-                    const int d = db * 32 + col;
-                    va[db] = *reinterpret_cast<const bf16x8*>(vt + d * kVPitch +
-                                                              ((8 * half + 16 * j) ^ (8 * vt_swizzle<KT>(d))));
-                }
+                    va[db] = *reinterpret_cast<const bf16x8*>(vt + db * 32 * kVPitch + ((16 * j) ^ (16 * db)));
 #pragma unroll
                 for (int db = 0; db < 4; db++)
                     o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[db], pb[j], o[db], 0, 0, 0);
