@@ -244,6 +244,63 @@ int awa_stack_block_times(const awa_stack* stack, float* attention_ms, float* bl
 /* Algorithmic FLOPs of each block: sum over windows of 4 * L^2 * head_dim * heads. */
 int awa_stack_block_flops(const awa_stack* stack, double* flops);
 
+/* ---- DiT block: the layers around the AWA chain ---- */
+
+/* One DiT block as the reference runs it per block (the ncnn graph exported
+ * from FixedDitBlock, tools/reference/dit_block.py:302-378, run through
+ * Extractor in0/in1/in2 -> out0/out1 by DitStackSession::run,
+ * src/dit/dit_stack.cpp:951-963): RMSNorm + Ada "in", the QKV projection, the
+ * AWA layer with the q/k RMSNorm fused (awa_forward_qknorm), the output
+ * projection + bias, Ada gate + residual, RMSNorm + Ada "in" (mlp), the SwiGLU
+ * MLP (tools/reference/dit_block.py:193-207) and Ada gate + residual, for the
+ * video and the text branch. A last block (is_last_layer) modulates and runs
+ * the MLP on video only and returns 2 * (text after attention + text).
+ * precision AWA_COMPUTE_F32: fp32 activations, GEMM weights and GEMMs (the
+ * FP32 prefix blocks); AWA_COMPUTE_BF16: bf16 activations and GEMM weights,
+ * fp32 accumulation and arithmetic (the BF16 blocks, dit_stack.cpp:519,
+ * :550). The GEMMs are library GEMMs (rocBLAS). */
+typedef struct awa_dit_block_desc {
+    int source_t, source_h, source_w;    /* token grid */
+    int windows_t, windows_h, windows_w; /* window counts (params 3/4/5) */
+    int text_tokens;
+    int shifted;
+    int heads, head_dim;  /* 20, 128 (head_dim must be 128) */
+    int hidden;           /* vid_dim = txt_dim, 2560 */
+    int mlp_hidden;       /* SwiGLU hidden width, 6912 for hidden 2560 */
+    int last_layer;
+    int precision;        /* AWA_COMPUTE_F32 or AWA_COMPUTE_BF16 */
+    float norm_eps;       /* 1e-5 */
+} awa_dit_block_desc;
+
+/* Device weights of one branch (video or text). GEMM weights are row-major
+ * [out][in] (torch Linear layout) in the block's precision; the rest is fp32.
+ * ada holds AdaSingle's learned vectors (dit_block.py:166-172) as 6 rows of
+ * hidden: attn shift, scale, gate, then mlp shift, scale, gate. The last
+ * block's text branch only needs qkv, proj_out, proj_out_bias, norm_q, norm_k. */
+typedef struct awa_dit_branch_weights {
+    const void* qkv;            /* [3*heads*head_dim][hidden] */
+    const void* proj_out;       /* [hidden][heads*head_dim] */
+    const float* proj_out_bias; /* [hidden] */
+    const void* mlp_gate;       /* [mlp_hidden][hidden] (proj_in_gate) */
+    const void* mlp_in;         /* [mlp_hidden][hidden] (proj_in) */
+    const void* mlp_out;        /* [hidden][mlp_hidden] (proj_out) */
+    const float* norm_q;        /* [head_dim], 16-byte aligned */
+    const float* norm_k;        /* [head_dim], 16-byte aligned */
+    const float* ada;           /* [6][hidden] */
+} awa_dit_branch_weights;
+
+typedef struct awa_dit_block awa_dit_block;
+
+int awa_dit_block_create(const awa_dit_block_desc* desc, awa_dit_block** block);
+void awa_dit_block_destroy(awa_dit_block* block);
+/* video [N][hidden], text [T_x][hidden] and the block embedding emb
+ * [hidden*6] (read as [hidden][2][3]: attn/mlp x shift/scale/gate) are dense
+ * device arrays in the block's precision, as are video_out and text_out
+ * (which must not alias the inputs). Asynchronous on stream. */
+int awa_dit_block_forward(awa_dit_block* block, const awa_dit_branch_weights* video_weights,
+                          const awa_dit_branch_weights* text_weights, const void* video, const void* text,
+                          const void* emb, void* video_out, void* text_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

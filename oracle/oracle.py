@@ -263,3 +263,86 @@ def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
 def round_bf16(x: np.ndarray) -> np.ndarray:
     """fp32 values rounded to the nearest bf16 (ties to even), returned as fp32."""
     return bf16_bits_to_f32(round_bf16_bits(x))
+
+
+# ---- DiT block around the AWA layer (tools/reference/dit_block.py:166-207, :344-378) ----
+
+@dataclass
+class DitBranchWeights:
+    """One branch's weights as fp32 host arrays: GEMM weights row-major
+    [out][in] (torch Linear), proj_out_bias [hidden], norm_q / norm_k
+    [head_dim], ada [6][hidden] (attn shift, scale, gate, mlp shift, scale,
+    gate: AdaSingle's learned vectors, dit_block.py:166-172)."""
+    qkv: np.ndarray
+    proj_out: np.ndarray
+    proj_out_bias: np.ndarray
+    mlp_gate: np.ndarray
+    mlp_in: np.ndarray
+    mlp_out: np.ndarray
+    norm_q: np.ndarray
+    norm_k: np.ndarray
+    ada: np.ndarray
+
+
+def ada_vectors(emb: np.ndarray, ada: np.ndarray, layer: int):
+    """(shift, scale, gate) of layer 0 (attn) or 1 (mlp): the block embedding
+    read as [hidden][2][3] plus the branch's learned vectors
+    (FixedAdaBranch.forward, dit_block.py:174-181)."""
+    e = np.asarray(emb, np.float64).reshape(-1, 2, 3)[:, layer, :]
+    a = np.asarray(ada, np.float64)
+    return e[:, 0] + a[3 * layer], e[:, 1] + a[3 * layer + 1], e[:, 2] + a[3 * layer + 2]
+
+
+def _rms(x: np.ndarray, eps: float) -> np.ndarray:
+    """nn.RMSNorm without affine over the last axis: x / sqrt(mean(x^2) + eps)."""
+    x = np.asarray(x, np.float64)
+    return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+
+
+def dit_block(g: Geometry, video: np.ndarray, text: np.ndarray, emb: np.ndarray, wv: DitBranchWeights,
+              wt: DitBranchWeights, heads: int, head_dim: int, eps: float, last_layer: bool, bf16: bool = False):
+    """FixedDitBlock.forward (dit_block.py:344-378) for one block: video
+    [N][hidden], text [T_x][hidden], emb [hidden*6]. Arithmetic is float64
+    except the AWA layer, which is the fp32 oracle above (q/k RMSNorm, then
+    Pack -> MMRoPE -> WindowAttention -> Unpack). With bf16=True the values are
+    rounded to bf16 where the bf16 DiT block stores them: the inputs, the
+    GEMM weights, and the output of every fused step (norm + Ada in, each
+    GEMM before its bias, the AWA layer, gate + residual, SwiGLU)."""
+    r = (lambda x: round_bf16(np.asarray(x, np.float32)).astype(np.float64)) if bf16 else \
+        (lambda x: np.asarray(x, np.float64))
+    wts = (wv, wt)
+    xs = (r(video), r(text))
+    modulate = (True, not last_layer)
+    hd = heads * head_dim
+
+    def lin(x, w):
+        return r(x @ r(w).T)
+
+    qkv = []
+    for br in range(2):
+        xa = _rms(xs[br], eps)
+        if modulate[br]:
+            shift, scale, _ = ada_vectors(r(emb), wts[br].ada, 0)
+            xa = xa * scale + shift
+        qkv.append(lin(r(xa), wts[br].qkv).reshape(-1, 3, heads, head_dim))
+    gammas = (wv.norm_q, wv.norm_k, wt.norm_q, wt.norm_k)
+    qv, qt = qk_norm_inputs(qkv[0].astype(np.float32), qkv[1].astype(np.float32), gammas, eps)
+    av, at = awa_layer(g, qv, qt, heads, head_dim)
+    att = (r(av.reshape(-1, hd)), r(at.reshape(-1, hd)))
+    outs = []
+    for br in range(2):
+        w = wts[br]
+        h = lin(att[br], w.proj_out) + np.asarray(w.proj_out_bias, np.float64)
+        if not modulate[br]:
+            y = r(h + xs[br])
+            outs.append(r(y + y))  # the last block's text: txt_attn + txt_attn
+            continue
+        _, _, gate = ada_vectors(r(emb), w.ada, 0)
+        y = r(h * gate + xs[br])
+        shift, scale, gate = ada_vectors(r(emb), w.ada, 1)
+        xm = r(_rms(y, eps) * scale + shift)
+        a = lin(xm, w.mlp_gate)
+        b = lin(xm, w.mlp_in)
+        hidden = r(a / (1.0 + np.exp(-a)) * b)
+        outs.append(r(lin(hidden, w.mlp_out) * gate + y))
+    return outs[0], outs[1]

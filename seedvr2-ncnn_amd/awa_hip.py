@@ -37,7 +37,7 @@ EXPORTED_SYMBOLS = (
     "awa_qkv_shape", "awa_forward", "awa_forward_qknorm", "awa_rmsnorm", "awa_pack", "awa_mmrope",
     "awa_window_attention", "awa_unpack", "awa_cast",
     "awa_stack_create", "awa_stack_destroy", "awa_stack_run", "awa_stack_set_profiling", "awa_stack_set_graph", "awa_stack_block_times",
-    "awa_stack_block_flops",
+    "awa_stack_block_flops", "awa_dit_block_create", "awa_dit_block_destroy", "awa_dit_block_forward",
 )
 
 
@@ -77,6 +77,19 @@ class AwaStackDesc(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int) for name in (
         "source_t", "source_h", "source_w", "windows_t", "windows_h", "windows_w", "text_tokens", "blocks",
         "fp32_prefix_blocks", "heads", "head_dim")]
+
+
+class AwaDitBlockDesc(ctypes.Structure):
+    """awa_dit_block_desc."""
+    _fields_ = [(name, ctypes.c_int) for name in (
+        "source_t", "source_h", "source_w", "windows_t", "windows_h", "windows_w", "text_tokens", "shifted",
+        "heads", "head_dim", "hidden", "mlp_hidden", "last_layer", "precision")] + [("norm_eps", ctypes.c_float)]
+
+
+class AwaDitBranchWeights(ctypes.Structure):
+    """awa_dit_branch_weights: device pointers of one branch's weights."""
+    _fields_ = [(name, ctypes.c_void_p) for name in (
+        "qkv", "proj_out", "proj_out_bias", "mlp_gate", "mlp_in", "mlp_out", "norm_q", "norm_k", "ada")]
 
 
 class AwaPlanInfo(ctypes.Structure):
@@ -140,6 +153,11 @@ def lib() -> ctypes.CDLL:
         L.awa_stack_set_profiling.argtypes = [vp, i]
         L.awa_stack_block_times.argtypes = [vp, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float)]
         L.awa_stack_block_flops.argtypes = [vp, ctypes.POINTER(ctypes.c_double)]
+        L.awa_dit_block_create.argtypes = [ctypes.POINTER(AwaDitBlockDesc), ctypes.POINTER(vp)]
+        L.awa_dit_block_destroy.argtypes = [vp]
+        L.awa_dit_block_destroy.restype = None
+        wp = ctypes.POINTER(AwaDitBranchWeights)
+        L.awa_dit_block_forward.argtypes = [vp, wp, wp, vp, vp, vp, vp, vp, vp]
         _LIB = L
     return _LIB
 
@@ -374,6 +392,37 @@ class Plan:
     def unpack(self, packed: AwaBlob, video_out: AwaBlob, text_out: AwaBlob, stream: Optional[Stream] = None) -> None:
         check(lib().awa_unpack(self.h, ctypes.byref(packed), ctypes.byref(video_out), ctypes.byref(text_out),
                                _s(stream)), "awa_unpack")
+
+
+class DitBlock:
+    """One DiT block around the AWA layer (awa_dit_block_*)."""
+
+    def __init__(self, t: int, h: int, w: int, nt: int, nh: int, nw: int, text_tokens: int, shifted: bool,
+                 heads: int, head_dim: int, hidden: int, mlp_hidden: int, last_layer: bool, precision: int,
+                 norm_eps: float = 1e-5):
+        self.desc = AwaDitBlockDesc(t, h, w, nt, nh, nw, text_tokens, int(shifted), heads, head_dim, hidden,
+                                    mlp_hidden, int(last_layer), precision, norm_eps)
+        p = ctypes.c_void_p()
+        check(lib().awa_dit_block_create(ctypes.byref(self.desc), ctypes.byref(p)), "awa_dit_block_create")
+        self.handle = p.value
+
+    def forward(self, video_weights: AwaDitBranchWeights, text_weights: AwaDitBranchWeights, video: int, text: int,
+                emb: int, video_out: int, text_out: int, stream: Optional["Stream"] = None) -> None:
+        check(lib().awa_dit_block_forward(ctypes.c_void_p(self.handle), ctypes.byref(video_weights),
+                                          ctypes.byref(text_weights), ctypes.c_void_p(video), ctypes.c_void_p(text),
+                                          ctypes.c_void_p(emb), ctypes.c_void_p(video_out),
+                                          ctypes.c_void_p(text_out), _s(stream)), "awa_dit_block_forward")
+
+    def destroy(self) -> None:
+        if self.handle:
+            lib().awa_dit_block_destroy(ctypes.c_void_p(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
 
 
 class AttentionStack:

@@ -1,0 +1,352 @@
+// One DiT block around the AWA layer (tools/reference/dit_block.py:344-378,
+// FixedDitBlock.forward; exported to the ncnn graph the reference runs per
+// block, src/dit/dit_stack.cpp:951-963):
+//
+//   x_a   = rmsnorm(x) * (1 + ...) Ada "in" (attn)        rmsnorm_modulate kernel
+//   qkv   = x_a W_qkv^T                                    GEMM (rocBLAS)
+//   att   = AWA(q/k RMSNorm(qkv))                          awa_forward_qknorm
+//   y     = (att W_out^T + b) * gate_attn + x              GEMM + gate_residual kernel
+//   x_m   = rmsnorm(y) Ada "in" (mlp)                      rmsnorm_modulate kernel
+//   h     = silu(x_m W_gate^T) * (x_m W_in^T)              2 GEMMs into one buffer + swiglu kernel
+//   out   = (h W_mlp^T) * gate_mlp + y                     GEMM + gate_residual kernel
+//
+// for the video and the text branch; the last block modulates and runs the
+// MLP on video only and returns text as 2 * y_text. Precision follows the
+// block: fp32 blocks keep fp32 activations, weights and GEMMs; bf16 blocks
+// store activations and GEMM weights in bf16 (round to nearest even) and
+// accumulate in fp32. Parameter vectors (biases, gammas, Ada) are fp32.
+#include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
+
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "awa_internal.h"
+#include "dit_kernels.h"
+#include "seedvr2_awa.h"
+
+struct awa_dit_block
+{
+    awa_dit_block_desc desc{};
+    awa_plan* plan = nullptr;
+    rocblas_handle blas = nullptr;
+    int es = 4; // activation / GEMM element size
+    int tokens[2] = {0, 0};
+    // Workspace per branch: normalised input, QKV, attention output, GEMM
+    // output, post-attention residual, MLP hidden pair, SwiGLU output.
+    void* ws[2][7] = {};
+};
+
+namespace
+{
+
+enum Buf
+{
+    kNorm = 0,
+    kQkv,
+    kAtt,
+    kGemm,
+    kResid,
+    kPair,
+    kHidden
+};
+
+int fail(int code, const std::string& message)
+{
+    awa::set_error(message);
+    return code;
+}
+
+int fail_hip(hipError_t e, const char* what)
+{
+    awa::set_error(std::string(what) + ": " + hipGetErrorString(e));
+    return AWA_ERR_DEVICE;
+}
+
+#define DIT_HIP(expr, what)                 \
+    do                                      \
+    {                                       \
+        const hipError_t e_ = (expr);       \
+        if (e_ != hipSuccess)               \
+            return fail_hip(e_, what);      \
+    } while (0)
+
+void release(awa_dit_block* b)
+{
+    for (auto& branch : b->ws)
+        for (void*& p : branch)
+        {
+            if (p)
+                (void)hipFree(p);
+            p = nullptr;
+        }
+    if (b->blas)
+        rocblas_destroy_handle(b->blas);
+    b->blas = nullptr;
+    if (b->plan)
+        awa_plan_destroy(b->plan);
+    b->plan = nullptr;
+}
+
+awa_blob dense3(void* data, int w, int h, int c, int elemsize)
+{
+    awa_blob m{};
+    m.data = data;
+    m.dims = 3;
+    m.w = w;
+    m.h = h;
+    m.d = 1;
+    m.c = c;
+    m.n = 1;
+    m.elemsize = elemsize;
+    m.cstep = static_cast<long long>(w) * h;
+    m.nstep = m.cstep * c;
+    return m;
+}
+
+// Y[M][N] (row stride ldy) = X[M][K] (row stride ldx) W[N][K]^T, fp32 accumulation.
+int gemm(awa_dit_block* b, const void* x, long long ldx, const void* w, void* y, long long ldy, int M, int N, int K,
+         hipStream_t stream)
+{
+    if (M <= 0)
+        return AWA_OK;
+    if (rocblas_set_stream(b->blas, stream) != rocblas_status_success)
+        return fail(AWA_ERR_DEVICE, "rocblas_set_stream failed");
+    const float alpha = 1.f, beta = 0.f;
+    const rocblas_datatype t = b->es == 2 ? rocblas_datatype_bf16_r : rocblas_datatype_f32_r;
+    // Column-major view: Y^T (N x M, ld ldy) = W (N x K from the K x N
+    // column-major W^T, transposed) * X^T (K x M, ld ldx).
+    const rocblas_status st =
+        rocblas_gemm_ex(b->blas, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &alpha, w, t, K, x, t,
+                        static_cast<rocblas_int>(ldx), &beta, y, t, static_cast<rocblas_int>(ldy), y, t,
+                        static_cast<rocblas_int>(ldy), rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+    if (st != rocblas_status_success)
+        return fail(AWA_ERR_DEVICE, std::string("rocblas_gemm_ex failed: ") + rocblas_status_to_string(st));
+    return AWA_OK;
+}
+
+bool branch_weights_valid(const awa_dit_branch_weights* w, bool full)
+{
+    if (!w || !w->qkv || !w->proj_out || !w->proj_out_bias || !w->norm_q || !w->norm_k)
+        return false;
+    if (full && (!w->mlp_gate || !w->mlp_in || !w->mlp_out || !w->ada))
+        return false;
+    return true;
+}
+
+} // namespace
+
+extern "C" {
+
+int awa_dit_block_create(const awa_dit_block_desc* desc, awa_dit_block** out)
+{
+    if (!desc || !out)
+        return fail(AWA_ERR_INVALID, "null argument");
+    *out = nullptr;
+    if (desc->heads <= 0 || desc->head_dim != 128 || desc->hidden <= 0 || desc->mlp_hidden <= 0 ||
+        (desc->precision != AWA_COMPUTE_F32 && desc->precision != AWA_COMPUTE_BF16) || !(desc->norm_eps >= 0.f) ||
+        desc->hidden % 8 || desc->mlp_hidden % 8)
+        return fail(AWA_ERR_INVALID, "invalid DiT block description (head_dim must be 128, widths multiples of 8)");
+    awa_dit_block* b = new (std::nothrow) awa_dit_block;
+    if (!b)
+        return fail(AWA_ERR_ALLOC, "block allocation failed");
+    b->desc = *desc;
+    b->es = desc->precision == AWA_COMPUTE_BF16 ? 2 : 4;
+    awa_plan_desc pd{};
+    pd.source_t = desc->source_t;
+    pd.source_h = desc->source_h;
+    pd.source_w = desc->source_w;
+    pd.windows_t = desc->windows_t;
+    pd.windows_h = desc->windows_h;
+    pd.windows_w = desc->windows_w;
+    pd.text_tokens = desc->text_tokens;
+    pd.shifted = desc->shifted;
+    pd.rope_dim = 126;
+    int rc = awa_plan_create(&pd, &b->plan);
+    if (rc != AWA_OK || (rc = awa_plan_upload(b->plan, nullptr)) != AWA_OK)
+    {
+        release(b);
+        delete b;
+        return rc;
+    }
+    if (rocblas_create_handle(&b->blas) != rocblas_status_success)
+    {
+        release(b);
+        delete b;
+        return fail(AWA_ERR_DEVICE, "rocblas_create_handle failed");
+    }
+    b->tokens[0] = desc->source_t * desc->source_h * desc->source_w;
+    b->tokens[1] = desc->text_tokens;
+    const long long hd = static_cast<long long>(desc->heads) * desc->head_dim;
+    for (int br = 0; br < 2; br++)
+    {
+        const long long M = b->tokens[br];
+        const long long widths[7] = {desc->hidden, 3 * hd, hd, desc->hidden, desc->hidden, 2LL * desc->mlp_hidden,
+                                     desc->mlp_hidden};
+        for (int k = 0; k < 7; k++)
+            if (hipMalloc(&b->ws[br][k], static_cast<size_t>(M * widths[k] * b->es)) != hipSuccess)
+            {
+                release(b);
+                delete b;
+                return fail(AWA_ERR_ALLOC, "DiT block workspace allocation failed");
+            }
+    }
+    *out = b;
+    return AWA_OK;
+}
+
+void awa_dit_block_destroy(awa_dit_block* b)
+{
+    if (!b)
+        return;
+    release(b);
+    delete b;
+}
+
+int awa_dit_block_forward(awa_dit_block* b, const awa_dit_branch_weights* video_w,
+                          const awa_dit_branch_weights* text_w, const void* video, const void* text, const void* emb,
+                          void* video_out, void* text_out, void* stream_ptr)
+{
+    if (!b || !video || !text || !emb || !video_out || !text_out)
+        return fail(AWA_ERR_INVALID, "null argument");
+    const awa_dit_block_desc& d = b->desc;
+    const bool last = d.last_layer != 0;
+    if (!branch_weights_valid(video_w, true) || !branch_weights_valid(text_w, !last))
+        return fail(AWA_ERR_INVALID, "missing DiT block weights");
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    const int es = b->es;
+    const int hidden = d.hidden;
+    const int hd = d.heads * d.head_dim;
+    const int mh = d.mlp_hidden;
+    const awa_dit_branch_weights* W[2] = {video_w, text_w};
+    const void* in[2] = {video, text};
+    void* out[2] = {video_out, text_out};
+    int rc;
+
+    // Attention half: norm + Ada in, QKV projection.
+    for (int br = 0; br < 2; br++)
+    {
+        const int M = b->tokens[br];
+        const bool modulate = br == 0 || !last;
+        awa::RowNormModulate nm{};
+        nm.in = in[br];
+        nm.in_elemsize = es;
+        nm.in_stride = hidden;
+        nm.out = b->ws[br][kNorm];
+        nm.out_elemsize = es;
+        nm.out_stride = hidden;
+        nm.rows = M;
+        nm.width = hidden;
+        nm.eps = d.norm_eps;
+        nm.emb = emb;
+        nm.emb_elemsize = es;
+        nm.layer = 0;
+        nm.shift_b = modulate ? W[br]->ada + 0 * hidden : nullptr;
+        nm.scale_b = modulate ? W[br]->ada + 1 * hidden : nullptr;
+        DIT_HIP(awa::launch_rmsnorm_modulate(nm, stream), "rmsnorm_modulate launch");
+        if ((rc = gemm(b, b->ws[br][kNorm], hidden, W[br]->qkv, b->ws[br][kQkv], 3LL * hd, M, 3 * hd, hidden,
+                       stream)) != AWA_OK)
+            return rc;
+    }
+    // AWA with the q/k RMSNorm fused into its gather.
+    {
+        const awa_blob vq = dense3(b->ws[0][kQkv], d.head_dim, 3 * d.heads, b->tokens[0], es);
+        const awa_blob tq = dense3(b->ws[1][kQkv], d.head_dim, 3 * d.heads, b->tokens[1], es);
+        const awa_blob vo = dense3(b->ws[0][kAtt], d.head_dim, d.heads, b->tokens[0], es);
+        const awa_blob to = dense3(b->ws[1][kAtt], d.head_dim, d.heads, b->tokens[1], es);
+        awa_qk_norm norm{video_w->norm_q, video_w->norm_k, text_w->norm_q, text_w->norm_k, d.norm_eps};
+        if ((rc = awa::forward_fused(b->plan, &vq, &tq, &norm, &vo, &to, d.precision, stream, nullptr)) != AWA_OK)
+            return rc;
+    }
+    for (int br = 0; br < 2; br++)
+    {
+        const int M = b->tokens[br];
+        const bool full = br == 0 || !last;
+        // Output projection, then bias, Ada gate (attn) and the residual.
+        if ((rc = gemm(b, b->ws[br][kAtt], hd, W[br]->proj_out, b->ws[br][kGemm], hidden, M, hidden, hd, stream)) !=
+            AWA_OK)
+            return rc;
+        awa::GateResidual gr{};
+        gr.h = b->ws[br][kGemm];
+        gr.h_elemsize = es;
+        gr.h_stride = hidden;
+        gr.bias = W[br]->proj_out_bias;
+        gr.residual = in[br];
+        gr.residual_elemsize = es;
+        gr.residual_stride = hidden;
+        gr.out = full ? b->ws[br][kResid] : out[br];
+        gr.out_elemsize = es;
+        gr.out_stride = hidden;
+        gr.rows = M;
+        gr.width = hidden;
+        gr.emb = emb;
+        gr.emb_elemsize = es;
+        gr.layer = 0;
+        gr.gate_b = full ? W[br]->ada + 2 * hidden : nullptr;
+        DIT_HIP(awa::launch_gate_residual(gr, stream), "gate_residual launch");
+        if (!full)
+        {
+            // Last block, text: out = 2 * (attention output + text).
+            DIT_HIP(awa::launch_double(out[br], es, hidden, out[br], es, hidden, M, hidden, stream), "double launch");
+            continue;
+        }
+        // MLP half: norm + Ada in (mlp), SwiGLU, output projection, gate + residual.
+        awa::RowNormModulate nm{};
+        nm.in = b->ws[br][kResid];
+        nm.in_elemsize = es;
+        nm.in_stride = hidden;
+        nm.out = b->ws[br][kNorm];
+        nm.out_elemsize = es;
+        nm.out_stride = hidden;
+        nm.rows = M;
+        nm.width = hidden;
+        nm.eps = d.norm_eps;
+        nm.emb = emb;
+        nm.emb_elemsize = es;
+        nm.layer = 1;
+        nm.shift_b = W[br]->ada + 3 * hidden;
+        nm.scale_b = W[br]->ada + 4 * hidden;
+        DIT_HIP(awa::launch_rmsnorm_modulate(nm, stream), "rmsnorm_modulate launch");
+        char* pair = static_cast<char*>(b->ws[br][kPair]);
+        if ((rc = gemm(b, b->ws[br][kNorm], hidden, W[br]->mlp_gate, pair, 2LL * mh, M, mh, hidden, stream)) !=
+                AWA_OK ||
+            (rc = gemm(b, b->ws[br][kNorm], hidden, W[br]->mlp_in, pair + static_cast<size_t>(mh) * es, 2LL * mh, M,
+                       mh, hidden, stream)) != AWA_OK)
+            return rc;
+        awa::SwiGlu sg{};
+        sg.in = pair;
+        sg.in_elemsize = es;
+        sg.in_stride = 2LL * mh;
+        sg.out = b->ws[br][kHidden];
+        sg.out_elemsize = es;
+        sg.out_stride = mh;
+        sg.rows = M;
+        sg.width = mh;
+        DIT_HIP(awa::launch_swiglu(sg, stream), "swiglu launch");
+        if ((rc = gemm(b, b->ws[br][kHidden], mh, W[br]->mlp_out, b->ws[br][kGemm], hidden, M, hidden, mh,
+                       stream)) != AWA_OK)
+            return rc;
+        awa::GateResidual go{};
+        go.h = b->ws[br][kGemm];
+        go.h_elemsize = es;
+        go.h_stride = hidden;
+        go.bias = nullptr;
+        go.residual = b->ws[br][kResid];
+        go.residual_elemsize = es;
+        go.residual_stride = hidden;
+        go.out = out[br];
+        go.out_elemsize = es;
+        go.out_stride = hidden;
+        go.rows = M;
+        go.width = hidden;
+        go.emb = emb;
+        go.emb_elemsize = es;
+        go.layer = 1;
+        go.gate_b = W[br]->ada + 5 * hidden;
+        DIT_HIP(awa::launch_gate_residual(go, stream), "gate_residual launch");
+    }
+    return AWA_OK;
+}
+
+} // extern "C"

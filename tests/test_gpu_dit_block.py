@@ -1,0 +1,95 @@
+"""The DiT block around the AWA layer on the GPU (awa_dit_block_forward)
+against the oracle block (FixedDitBlock.forward restated,
+tools/reference/dit_block.py:344-378).
+
+Tolerances, max|err| / max|ref| over each output:
+- fp32 block: <= 1e-5. Everything is fp32 on the GPU against float64 in the
+  oracle; the AWA layer itself is held to 1e-4 absolute elsewhere, and its
+  output enters the block through a projection with weights ~0.05.
+- bf16 block: <= 2e-2 (the bf16 budget). The oracle rounds to bf16 at the
+  same points the GPU block stores bf16, so the remainder is accumulation
+  order and the bf16 attention arithmetic.
+"""
+
+import numpy as np
+import pytest
+
+import awa_hip as A
+import oracle as O
+from awa_cases import geometry
+from test_dit_block_oracle import EPS, HEAD_DIM, HEADS, HIDDEN, MLP, case
+
+pytestmark = pytest.mark.gpu
+
+
+class DeviceBranch:
+    """A branch's weights on the device: GEMM weights in the block's element size."""
+
+    def __init__(self, w: O.DitBranchWeights, elemsize: int):
+        self.bufs = []
+
+        def up(a, es):
+            a = np.ascontiguousarray(a, np.float32)
+            buf = A.DeviceBuffer(a.size * es)
+            buf.upload(A.f32_to_bf16_bits(a) if es == 2 else a)
+            self.bufs.append(buf)
+            return buf.ptr
+
+        self.struct = A.AwaDitBranchWeights(
+            up(w.qkv, elemsize), up(w.proj_out, elemsize), up(w.proj_out_bias, 4), up(w.mlp_gate, elemsize),
+            up(w.mlp_in, elemsize), up(w.mlp_out, elemsize), up(w.norm_q, 4), up(w.norm_k, 4), up(w.ada, 4))
+
+
+def upload_act(x, es):
+    x = np.ascontiguousarray(x, np.float32)
+    buf = A.DeviceBuffer(x.size * es)
+    buf.upload(A.f32_to_bf16_bits(x) if es == 2 else x)
+    return buf
+
+
+def download_act(buf, shape, es):
+    n = int(np.prod(shape))
+    if es == 2:
+        return A.bf16_bits_to_f32(buf.download((n,), np.uint16)).reshape(shape)
+    return buf.download((n,), np.float32).reshape(shape)
+
+
+def run_block(g, video, text, emb, wv, wt, last_layer, precision):
+    es = 2 if precision == A.COMPUTE_BF16 else 4
+    blk = A.DitBlock(*g.args, g.text_tokens, g.shifted, HEADS, HEAD_DIM, HIDDEN, MLP, last_layer, precision, EPS)
+    dv, dt = DeviceBranch(wv, es), DeviceBranch(wt, es)
+    bv, bt, be = upload_act(video, es), upload_act(text, es), upload_act(emb, es)
+    ov, ot = A.DeviceBuffer(video.size * es), A.DeviceBuffer(text.size * es)
+    blk.forward(dv.struct, dt.struct, bv.ptr, bt.ptr, be.ptr, ov.ptr, ot.ptr)
+    A.synchronize()
+    out = download_act(ov, video.shape, es), download_act(ot, text.shape, es)
+    blk.destroy()
+    return out
+
+
+def rel(a, b):
+    return float(np.max(np.abs(a.astype(np.float64) - b)) / np.max(np.abs(b)))
+
+
+@pytest.mark.parametrize("last_layer", [False, True])
+@pytest.mark.parametrize("shifted", [False, True])
+@pytest.mark.parametrize("precision", [A.COMPUTE_F32, A.COMPUTE_BF16])
+def test_dit_block_matches_oracle(gpu, precision, shifted, last_layer):
+    bf16 = precision == A.COMPUTE_BF16
+    print(f"case dit block bf16={bf16} shifted={shifted} last={last_layer}", flush=True)
+    g, video, text, emb, wv, wt = case(100 + 4 * bf16 + 2 * shifted + last_layer, shifted)
+    got_v, got_t = run_block(g, video, text, emb, wv, wt, last_layer, precision)
+    ref_v, ref_t = O.dit_block(g, video, text, emb, wv, wt, HEADS, HEAD_DIM, EPS, last_layer, bf16=bf16)
+    tol = 2e-2 if bf16 else 1e-5
+    ev, et = rel(got_v, ref_v), rel(got_t, ref_t)
+    print(f"  rel err video {ev:.3g} text {et:.3g}", flush=True)
+    assert ev <= tol and et <= tol
+
+
+def test_dit_block_rejects_bad_descriptions(gpu):
+    for kw in ({"head_dim": 64}, {"hidden": 250}, {"precision": 7}):
+        args = dict(t=2, h=16, w=16, nt=1, nh=8, nw=8, text_tokens=16, shifted=False, heads=HEADS,
+                    head_dim=HEAD_DIM, hidden=HIDDEN, mlp_hidden=MLP, last_layer=False, precision=A.COMPUTE_F32)
+        args.update(kw)
+        with pytest.raises(A.AwaError):
+            A.DitBlock(**args)
