@@ -138,6 +138,78 @@ def qk_prologue(A, bufs, stream, iters: int = 20) -> dict:
     return res
 
 
+MLP_HIDDEN = 6912  # SwiGLU hidden width for hidden 2560 (tools/reference/dit_block.py:195-197)
+
+
+def dit_step(A, stream, steps: int, warmup: int = 2) -> dict:
+    """The whole DiT step at the same workload: 32 full blocks (RMSNorm + Ada,
+    QKV projection, AWA with the fused q/k norm, output projection, gate +
+    residual, SwiGLU MLP, gate + residual; video and text branches; the last
+    block video-only) with blocks 0-8 in fp32 and 9-31 in bf16. Random-init
+    weights N(0, 0.02) (Ada vectors and gammas included), fp32 inputs N(0, 1),
+    all resident on the device before timing. ms per step over `steps` steps
+    (HIP events), per-block times from a profiled step, and the GEMM + attention
+    FLOPs of the step."""
+    t, h, w = GRID
+    N = t * h * w
+    hidden, hd, mh = HEADS * HEAD_DIM, HEADS * HEAD_DIM, MLP_HIDDEN
+    stack = A.DitStack(t, h, w, *WINDOWS, TEXT, BLOCKS, FP32_PREFIX, HEADS, HEAD_DIM, hidden, mh)
+    keep = []
+    seed = [9000]
+
+    def buf(count, es, stddev=0.02):
+        b = A.DeviceBuffer(count * es)
+        b.fill_normal(count, es, seed[0], stream, stddev)
+        seed[0] += 1
+        keep.append(b)
+        return b.ptr
+
+    wv, wt = [], []
+    for b in range(BLOCKS):
+        es = 4 if b < FP32_PREFIX else 2
+        for lst in (wv, wt):
+            lst.append(A.AwaDitBranchWeights(
+                buf(3 * hd * hidden, es), buf(hidden * hd, es), buf(hidden, 4), buf(mh * hidden, es),
+                buf(mh * hidden, es), buf(hidden * mh, es), buf(HEAD_DIM, 4), buf(HEAD_DIM, 4), buf(6 * hidden, 4)))
+    video, text, emb = buf(N * hidden, 4, 1.0), buf(TEXT * hidden, 4, 1.0), buf(6 * hidden, 4, 1.0)
+    vout, tout = buf(N * hidden, 2, 1.0), buf(TEXT * hidden, 2, 1.0)
+    stream.synchronize()
+    for _ in range(warmup):
+        stack.run(wv, wt, video, text, emb, vout, tout, stream)
+    e0, e1 = A.Event(), A.Event()
+    e0.record(stream)
+    for _ in range(steps):
+        stack.run(wv, wt, video, text, emb, vout, tout, stream)
+    e1.record(stream)
+    stream.synchronize()
+    ms = e0.elapsed_ms(e1) / steps
+    stack.set_profiling(True)
+    stack.run(wv, wt, video, text, emb, vout, tout, stream)
+    stream.synchronize()
+    per_block = stack.block_times()
+    stack.destroy()
+
+    def gemm_flops(m, last_text=False):
+        f = 2.0 * m * hidden * (3 * hd) + 2.0 * m * hd * hidden
+        return f if last_text else f + 3 * 2.0 * m * hidden * mh
+
+    att = A.AttentionStack(t, h, w, *WINDOWS, TEXT, BLOCKS, FP32_PREFIX, HEADS, HEAD_DIM)
+    att_flops = float(att.block_flops().sum())
+    att.destroy()
+    flops = BLOCKS * gemm_flops(N) + (BLOCKS - 1) * gemm_flops(TEXT) + gemm_flops(TEXT, True) + att_flops
+    return {
+        "ms_per_step": round(ms, 3),
+        "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+        "step_gflop": round(flops / 1e9, 1),
+        "fp32_block_ms": round(float(per_block[:FP32_PREFIX].mean()), 4),
+        "bf16_block_ms": round(float(per_block[FP32_PREFIX:].mean()), 4),
+        "steps": steps,
+        "config": "32 blocks, hidden 2560, SwiGLU 6912, 20x128 heads, latent 9x16x16, windows 3x8x8, 64 text; "
+                  "blocks 0-8 fp32, 9-31 bf16; GEMMs on rocBLAS",
+        "data": "random-init weights N(0, 0.02), inputs N(0, 1), synthetic",
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -145,6 +217,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--profile-steps", type=int, default=5, help="steps with per-block event timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-dit-step", action="store_true", help="skip the full 32-block DiT step measurement")
+    ap.add_argument("--dit-steps", type=int, default=5)
     ap.add_argument("--cpu-sample-layers", type=int, default=2, choices=(1, 2))
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "awa_attention_hbm_traffic.json"),
                     help="measured HBM bytes per launch of each attention kernel (rocprofv3 --pmc FETCH_SIZE and "
@@ -302,6 +376,9 @@ def main() -> int:
         },
     }
     result["qk_prologue"] = qk_prologue(A, buffers[FP32_PREFIX], stream)
+    if not args.no_dit_step:
+        del buffers, vq, tq, vo, to
+        result["dit_step"] = dit_step(A, stream, args.dit_steps)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_sample_layers)
     print(json.dumps(result), flush=True)

@@ -112,6 +112,9 @@ int awa_event_elapsed_ms(void* start, void* stop, float* ms);
  * elemsize 4 or 2 (bf16, rounded to nearest even). Used to build benchmark
  * inputs; parity tests use the host generator of the reference instead. */
 int awa_fill_normal(void* dst, size_t count, int elemsize, unsigned long long seed, void* stream);
+/* The same numbers times stddev (random-init weights, e.g. N(0, 0.02)). */
+int awa_fill_normal_scaled(void* dst, size_t count, int elemsize, unsigned long long seed, float stddev,
+                           void* stream);
 
 /* ---- plan: windows, index maps, RoPE tables (the layers' load_param/upload_model) ---- */
 
@@ -300,6 +303,41 @@ void awa_dit_block_destroy(awa_dit_block* block);
 int awa_dit_block_forward(awa_dit_block* block, const awa_dit_branch_weights* video_weights,
                           const awa_dit_branch_weights* text_weights, const void* video, const void* text,
                           const void* emb, void* video_out, void* text_out, void* stream);
+
+/* The block loop of a DiT step: DitStackSession::run (src/dit/dit_stack.cpp:931-982)
+ * over full blocks. Blocks [0, fp32_prefix_blocks) run fp32, the rest bf16;
+ * at the first bf16 block the carried video and text and the embedding are
+ * cast to bf16 once (:934-950). Even blocks use unshifted windows, odd
+ * blocks shifted (tools/reference/dit_stack.py:75-79); the last block is the
+ * is_last_layer variant (tools/reference/dit_stack.py, dit_block.py:324). */
+typedef struct awa_dit_stack_desc {
+    int source_t, source_h, source_w;
+    int windows_t, windows_h, windows_w;
+    int text_tokens;
+    int blocks;             /* 32 */
+    int fp32_prefix_blocks; /* 9 */
+    int heads, head_dim;    /* 20, 128 */
+    int hidden, mlp_hidden; /* 2560, 6912 */
+    float norm_eps;         /* 1e-5 */
+} awa_dit_stack_desc;
+
+typedef struct awa_dit_stack awa_dit_stack;
+
+int awa_dit_stack_create(const awa_dit_stack_desc* desc, awa_dit_stack** stack);
+void awa_dit_stack_destroy(awa_dit_stack* stack);
+/* video_weights / text_weights: one struct per block, in each block's
+ * precision (awa_dit_branch_weights). video [N][hidden], text [T_x][hidden]
+ * and emb [hidden*6] are fp32 (the inputs of block 0, which is fp32 unless
+ * fp32_prefix_blocks is 0); video_out / text_out take the last block's
+ * outputs in its precision. Asynchronous on stream. */
+int awa_dit_stack_run(awa_dit_stack* stack, const awa_dit_branch_weights* video_weights,
+                      const awa_dit_branch_weights* text_weights, const void* video, const void* text,
+                      const void* emb, void* video_out, void* text_out, void* stream);
+/* Per-block timing (the reference's --profile surface): when enabled each run
+ * records an event before every block and after the last. */
+int awa_dit_stack_set_profiling(awa_dit_stack* stack, int enabled);
+/* After a profiled run has completed: milliseconds of each block. */
+int awa_dit_stack_block_times(const awa_dit_stack* stack, float* block_ms);
 
 #ifdef __cplusplus
 }

@@ -31,13 +31,15 @@ EXPORTED_SYMBOLS = (
     "awa_last_error", "awa_device_count", "awa_runtime_init", "awa_malloc", "awa_free", "awa_host_alloc",
     "awa_host_free", "awa_memcpy_h2d", "awa_memcpy_d2h", "awa_memcpy_d2d", "awa_zero", "awa_stream_create",
     "awa_stream_destroy", "awa_stream_synchronize", "awa_event_create", "awa_event_destroy", "awa_event_record",
-    "awa_event_synchronize", "awa_event_elapsed_ms", "awa_fill_normal", "awa_plan_create", "awa_plan_destroy",
+    "awa_event_synchronize", "awa_event_elapsed_ms", "awa_fill_normal", "awa_fill_normal_scaled", "awa_plan_create", "awa_plan_destroy",
     "awa_plan_info_get", "awa_plan_windows", "awa_plan_sequence_index", "awa_plan_cu_seqlens",
     "awa_plan_video_positions", "awa_plan_text_positions", "awa_plan_rope_table", "awa_plan_upload",
     "awa_qkv_shape", "awa_forward", "awa_forward_qknorm", "awa_rmsnorm", "awa_pack", "awa_mmrope",
     "awa_window_attention", "awa_unpack", "awa_cast",
     "awa_stack_create", "awa_stack_destroy", "awa_stack_run", "awa_stack_set_profiling", "awa_stack_set_graph", "awa_stack_block_times",
     "awa_stack_block_flops", "awa_dit_block_create", "awa_dit_block_destroy", "awa_dit_block_forward",
+    "awa_dit_stack_create", "awa_dit_stack_destroy", "awa_dit_stack_run", "awa_dit_stack_set_profiling",
+    "awa_dit_stack_block_times",
 )
 
 
@@ -86,6 +88,13 @@ class AwaDitBlockDesc(ctypes.Structure):
         "heads", "head_dim", "hidden", "mlp_hidden", "last_layer", "precision")] + [("norm_eps", ctypes.c_float)]
 
 
+class AwaDitStackDesc(ctypes.Structure):
+    """awa_dit_stack_desc."""
+    _fields_ = [(name, ctypes.c_int) for name in (
+        "source_t", "source_h", "source_w", "windows_t", "windows_h", "windows_w", "text_tokens", "blocks",
+        "fp32_prefix_blocks", "heads", "head_dim", "hidden", "mlp_hidden")] + [("norm_eps", ctypes.c_float)]
+
+
 class AwaDitBranchWeights(ctypes.Structure):
     """awa_dit_branch_weights: device pointers of one branch's weights."""
     _fields_ = [(name, ctypes.c_void_p) for name in (
@@ -127,6 +136,7 @@ def lib() -> ctypes.CDLL:
         L.awa_event_synchronize.argtypes = [vp]
         L.awa_event_elapsed_ms.argtypes = [vp, vp, ctypes.POINTER(ctypes.c_float)]
         L.awa_fill_normal.argtypes = [vp, sz, i, ctypes.c_ulonglong, vp]
+        L.awa_fill_normal_scaled.argtypes = [vp, sz, i, ctypes.c_ulonglong, ctypes.c_float, vp]
         L.awa_plan_create.argtypes = [ctypes.POINTER(AwaPlanDesc), ctypes.POINTER(vp)]
         L.awa_plan_destroy.argtypes = [vp]
         L.awa_plan_destroy.restype = None
@@ -158,6 +168,12 @@ def lib() -> ctypes.CDLL:
         L.awa_dit_block_destroy.restype = None
         wp = ctypes.POINTER(AwaDitBranchWeights)
         L.awa_dit_block_forward.argtypes = [vp, wp, wp, vp, vp, vp, vp, vp, vp]
+        L.awa_dit_stack_create.argtypes = [ctypes.POINTER(AwaDitStackDesc), ctypes.POINTER(vp)]
+        L.awa_dit_stack_destroy.argtypes = [vp]
+        L.awa_dit_stack_destroy.restype = None
+        L.awa_dit_stack_run.argtypes = [vp, wp, wp, vp, vp, vp, vp, vp, vp]
+        L.awa_dit_stack_set_profiling.argtypes = [vp, i]
+        L.awa_dit_stack_block_times.argtypes = [vp, ctypes.POINTER(ctypes.c_float)]
         _LIB = L
     return _LIB
 
@@ -224,9 +240,10 @@ class DeviceBuffer:
     def zero(self, stream: Optional["Stream"] = None) -> None:
         check(lib().awa_zero(ctypes.c_void_p(self.ptr), self.nbytes, _s(stream)), "awa_zero")
 
-    def fill_normal(self, count: int, elemsize: int, seed: int, stream: Optional["Stream"] = None) -> None:
-        check(lib().awa_fill_normal(ctypes.c_void_p(self.ptr), count, elemsize, seed, _s(stream)),
-              "awa_fill_normal")
+    def fill_normal(self, count: int, elemsize: int, seed: int, stream: Optional["Stream"] = None,
+                    stddev: float = 1.0) -> None:
+        check(lib().awa_fill_normal_scaled(ctypes.c_void_p(self.ptr), count, elemsize, seed, stddev, _s(stream)),
+              "awa_fill_normal_scaled")
 
 
 class Stream:
@@ -416,6 +433,49 @@ class DitBlock:
     def destroy(self) -> None:
         if self.handle:
             lib().awa_dit_block_destroy(ctypes.c_void_p(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+class DitStack:
+    """The DiT step's block loop (awa_dit_stack_*): full blocks with the fp32/bf16 dispatch."""
+
+    def __init__(self, t: int, h: int, w: int, nt: int, nh: int, nw: int, text_tokens: int, blocks: int,
+                 fp32_prefix_blocks: int, heads: int, head_dim: int, hidden: int, mlp_hidden: int,
+                 norm_eps: float = 1e-5):
+        self.desc = AwaDitStackDesc(t, h, w, nt, nh, nw, text_tokens, blocks, fp32_prefix_blocks, heads, head_dim,
+                                    hidden, mlp_hidden, norm_eps)
+        p = ctypes.c_void_p()
+        check(lib().awa_dit_stack_create(ctypes.byref(self.desc), ctypes.byref(p)), "awa_dit_stack_create")
+        self.handle = p.value
+        self.blocks = blocks
+
+    def run(self, video_weights: Sequence[AwaDitBranchWeights], text_weights: Sequence[AwaDitBranchWeights],
+            video: int, text: int, emb: int, video_out: int, text_out: int,
+            stream: Optional["Stream"] = None) -> None:
+        arr = AwaDitBranchWeights * self.blocks
+        check(lib().awa_dit_stack_run(ctypes.c_void_p(self.handle), arr(*video_weights), arr(*text_weights),
+                                      ctypes.c_void_p(video), ctypes.c_void_p(text), ctypes.c_void_p(emb),
+                                      ctypes.c_void_p(video_out), ctypes.c_void_p(text_out), _s(stream)),
+              "awa_dit_stack_run")
+
+    def set_profiling(self, enabled: bool) -> None:
+        check(lib().awa_dit_stack_set_profiling(ctypes.c_void_p(self.handle), int(enabled)),
+              "awa_dit_stack_set_profiling")
+
+    def block_times(self) -> np.ndarray:
+        t = (ctypes.c_float * self.blocks)()
+        check(lib().awa_dit_stack_block_times(ctypes.c_void_p(self.handle), t), "awa_dit_stack_block_times")
+        return np.array(t[:], np.float64)
+
+    def destroy(self) -> None:
+        if self.handle:
+            lib().awa_dit_stack_destroy(ctypes.c_void_p(self.handle))
             self.handle = None
 
     def __del__(self):

@@ -470,10 +470,16 @@ int awa_event_elapsed_ms(void* start, void* stop, float* ms)
 
 int awa_fill_normal(void* dst, size_t count, int elemsize, unsigned long long seed, void* stream)
 {
-    if ((count && !dst) || (elemsize != 2 && elemsize != 4))
+    return awa_fill_normal_scaled(dst, count, elemsize, seed, 1.f, stream);
+}
+
+int awa_fill_normal_scaled(void* dst, size_t count, int elemsize, unsigned long long seed, float stddev,
+                           void* stream)
+{
+    if ((count && !dst) || (elemsize != 2 && elemsize != 4) || !std::isfinite(stddev))
         return fail(AWA_ERR_INVALID, "invalid fill arguments");
     if (count)
-        HIP_TRY(awa::launch_fill_normal(dst, count, elemsize, seed, as_stream(stream)), "fill kernel");
+        HIP_TRY(awa::launch_fill_normal(dst, count, elemsize, seed, stddev, as_stream(stream)), "fill kernel");
     return AWA_OK;
 }
 

@@ -114,7 +114,8 @@ hipError_t launch_rmsnorm(const void* in, int in_elemsize, long long in_cstep, v
 hipError_t launch_cast(const void* in, int in_elemsize, void* out, int out_elemsize, const CastShape& s,
                        hipStream_t stream);
 
-hipError_t launch_fill_normal(void* dst, size_t count, int elemsize, unsigned long long seed, hipStream_t stream);
+hipError_t launch_fill_normal(void* dst, size_t count, int elemsize, unsigned long long seed, float stddev,
+                              hipStream_t stream);
 hipError_t launch_zero(void* dst, size_t bytes, hipStream_t stream);
 
 } // namespace awa

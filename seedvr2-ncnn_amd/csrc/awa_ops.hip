@@ -338,7 +338,7 @@ __device__ __forceinline__ uint64_t splitmix64(uint64_t x)
     return x ^ (x >> 31);
 }
 
-__global__ void fill_normal_kernel(void* dst, size_t count, int elemsize, unsigned long long seed)
+__global__ void fill_normal_kernel(void* dst, size_t count, int elemsize, unsigned long long seed, float stddev)
 {
     const size_t pair = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const size_t i0 = 2 * pair;
@@ -350,9 +350,9 @@ __global__ void fill_normal_kernel(void* dst, size_t count, int elemsize, unsign
     const float radius = sqrtf(-2.f * logf(u1));
     float sn, cs;
     sincosf(6.283185307179586f * u2, &sn, &cs);
-    store_elem(dst, static_cast<long long>(i0), elemsize, radius * cs);
+    store_elem(dst, static_cast<long long>(i0), elemsize, stddev * (radius * cs));
     if (i0 + 1 < count)
-        store_elem(dst, static_cast<long long>(i0 + 1), elemsize, radius * sn);
+        store_elem(dst, static_cast<long long>(i0 + 1), elemsize, stddev * (radius * sn));
 }
 
 __global__ void zero_kernel(uint32_t* dst, size_t words, unsigned char* tail, size_t tail_bytes)
@@ -472,11 +472,12 @@ hipError_t launch_rmsnorm(const void* in, int in_elemsize, long long in_cstep, v
     return hipGetLastError();
 }
 
-hipError_t launch_fill_normal(void* dst, size_t count, int elemsize, unsigned long long seed, hipStream_t stream)
+hipError_t launch_fill_normal(void* dst, size_t count, int elemsize, unsigned long long seed, float stddev,
+                              hipStream_t stream)
 {
     const long long pairs = static_cast<long long>((count + 1) / 2);
     hipLaunchKernelGGL(fill_normal_kernel, dim3(grid_for(pairs)), dim3(kBlock), 0, stream, dst, count, elemsize,
-                       seed);
+                       seed, stddev);
     return hipGetLastError();
 }
 

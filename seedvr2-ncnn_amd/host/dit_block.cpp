@@ -21,6 +21,7 @@
 #include <cstring>
 #include <new>
 #include <string>
+#include <vector>
 
 #include "awa_internal.h"
 #include "dit_kernels.h"
@@ -346,6 +347,219 @@ int awa_dit_block_forward(awa_dit_block* b, const awa_dit_branch_weights* video_
         go.gate_b = W[br]->ada + 5 * hidden;
         DIT_HIP(awa::launch_gate_residual(go, stream), "gate_residual launch");
     }
+    return AWA_OK;
+}
+
+} // extern "C"
+
+// ---- The block loop: DitStackSession::run (src/dit/dit_stack.cpp:931-982) ----
+//
+// Blocks [0, fp32_prefix_blocks) run fp32, the rest bf16; at the first bf16
+// block the carried video, text and the embedding are cast to bf16 once
+// (convert_precision_gpu, :934-950). Even blocks use unshifted windows, odd
+// blocks shifted (tools/reference/dit_stack.py:75-79); the last block is the
+// is_last_layer variant. Activations ping-pong between two buffers per
+// precision; one block object (plan, GEMM handle, workspace) serves every
+// block of its (precision, shift) and the last block has its own.
+struct awa_dit_stack
+{
+    awa_dit_stack_desc desc{};
+    awa_dit_block* blocks[2][2] = {}; // [bf16][shifted]
+    awa_dit_block* last = nullptr;
+    void* act[2][2][2] = {};          // [bf16][ping][video, text]
+    void* emb_bf16 = nullptr;
+    int tokens[2] = {0, 0};
+    bool profiling = false;
+    std::vector<hipEvent_t> events; // blocks + 1
+};
+
+namespace
+{
+
+void release_stack(awa_dit_stack* s)
+{
+    for (auto& p : s->blocks)
+        for (awa_dit_block*& b : p)
+        {
+            awa_dit_block_destroy(b);
+            b = nullptr;
+        }
+    awa_dit_block_destroy(s->last);
+    s->last = nullptr;
+    for (auto& prec : s->act)
+        for (auto& ping : prec)
+            for (void*& p : ping)
+            {
+                if (p)
+                    (void)hipFree(p);
+                p = nullptr;
+            }
+    if (s->emb_bf16)
+        (void)hipFree(s->emb_bf16);
+    s->emb_bf16 = nullptr;
+    for (hipEvent_t e : s->events)
+        (void)hipEventDestroy(e);
+    s->events.clear();
+}
+
+int cast_rows(const void* in, int in_es, void* out, int out_es, int rows, int width, hipStream_t stream)
+{
+    awa_blob a = dense3(const_cast<void*>(in), width, rows, 1, in_es);
+    awa_blob b = dense3(out, width, rows, 1, out_es);
+    a.dims = b.dims = 2;
+    return awa_cast(&a, &b, stream);
+}
+
+} // namespace
+
+extern "C" {
+
+int awa_dit_stack_create(const awa_dit_stack_desc* desc, awa_dit_stack** out)
+{
+    if (!desc || !out)
+        return fail(AWA_ERR_INVALID, "null argument");
+    *out = nullptr;
+    if (desc->blocks <= 0 || desc->fp32_prefix_blocks < 0 || desc->fp32_prefix_blocks > desc->blocks)
+        return fail(AWA_ERR_INVALID, "invalid block counts");
+    awa_dit_stack* s = new (std::nothrow) awa_dit_stack;
+    if (!s)
+        return fail(AWA_ERR_ALLOC, "stack allocation failed");
+    s->desc = *desc;
+    s->tokens[0] = desc->source_t * desc->source_h * desc->source_w;
+    s->tokens[1] = desc->text_tokens;
+    auto block_desc = [&](bool bf16, bool shifted, bool last) {
+        awa_dit_block_desc b{};
+        b.source_t = desc->source_t;
+        b.source_h = desc->source_h;
+        b.source_w = desc->source_w;
+        b.windows_t = desc->windows_t;
+        b.windows_h = desc->windows_h;
+        b.windows_w = desc->windows_w;
+        b.text_tokens = desc->text_tokens;
+        b.shifted = shifted;
+        b.heads = desc->heads;
+        b.head_dim = desc->head_dim;
+        b.hidden = desc->hidden;
+        b.mlp_hidden = desc->mlp_hidden;
+        b.last_layer = last;
+        b.precision = bf16 ? AWA_COMPUTE_BF16 : AWA_COMPUTE_F32;
+        b.norm_eps = desc->norm_eps;
+        return b;
+    };
+    int rc = AWA_OK;
+    for (int bf = 0; bf < 2 && rc == AWA_OK; bf++)
+    {
+        // Only the precisions the loop uses.
+        const bool used = bf ? desc->fp32_prefix_blocks < desc->blocks - 1 : desc->fp32_prefix_blocks > 0;
+        for (int sh = 0; sh < 2 && rc == AWA_OK && used; sh++)
+        {
+            const awa_dit_block_desc bd = block_desc(bf, sh, false);
+            rc = awa_dit_block_create(&bd, &s->blocks[bf][sh]);
+        }
+    }
+    const int lb = desc->blocks - 1;
+    if (rc == AWA_OK)
+    {
+        const awa_dit_block_desc bd = block_desc(lb >= desc->fp32_prefix_blocks, lb % 2, true);
+        rc = awa_dit_block_create(&bd, &s->last);
+    }
+    for (int bf = 0; bf < 2 && rc == AWA_OK; bf++)
+        for (int ping = 0; ping < 2 && rc == AWA_OK; ping++)
+            for (int br = 0; br < 2; br++)
+                if (hipMalloc(&s->act[bf][ping][br],
+                              static_cast<size_t>(s->tokens[br]) * desc->hidden * (bf ? 2 : 4)) != hipSuccess)
+                {
+                    rc = fail(AWA_ERR_ALLOC, "stack activation allocation failed");
+                    break;
+                }
+    if (rc == AWA_OK && hipMalloc(&s->emb_bf16, static_cast<size_t>(desc->hidden) * 6 * 2) != hipSuccess)
+        rc = fail(AWA_ERR_ALLOC, "stack embedding allocation failed");
+    if (rc != AWA_OK)
+    {
+        release_stack(s);
+        delete s;
+        return rc;
+    }
+    *out = s;
+    return AWA_OK;
+}
+
+void awa_dit_stack_destroy(awa_dit_stack* s)
+{
+    if (!s)
+        return;
+    release_stack(s);
+    delete s;
+}
+
+int awa_dit_stack_set_profiling(awa_dit_stack* s, int enabled)
+{
+    if (!s)
+        return fail(AWA_ERR_INVALID, "null stack");
+    s->profiling = enabled != 0;
+    if (s->profiling && s->events.empty())
+    {
+        s->events.resize(s->desc.blocks + 1, nullptr);
+        for (hipEvent_t& e : s->events)
+            DIT_HIP(hipEventCreate(&e), "hipEventCreate");
+    }
+    return AWA_OK;
+}
+
+int awa_dit_stack_run(awa_dit_stack* s, const awa_dit_branch_weights* video_weights,
+                      const awa_dit_branch_weights* text_weights, const void* video, const void* text,
+                      const void* emb, void* video_out, void* text_out, void* stream_ptr)
+{
+    if (!s || !video_weights || !text_weights || !video || !text || !emb || !video_out || !text_out)
+        return fail(AWA_ERR_INVALID, "null argument");
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    const awa_dit_stack_desc& d = s->desc;
+    const void* cur[2] = {video, text};
+    const void* cur_emb = emb;
+    int ping = 0;
+    int rc;
+    for (int b = 0; b < d.blocks; b++)
+    {
+        const bool bf16 = b >= d.fp32_prefix_blocks;
+        if (bf16 && b == d.fp32_prefix_blocks)
+        {
+            // Precision switch: carried activations and the embedding to bf16.
+            for (int br = 0; br < 2; br++)
+            {
+                void* dst = s->act[1][ping][br];
+                if ((rc = cast_rows(cur[br], 4, dst, 2, s->tokens[br], d.hidden, stream)) != AWA_OK)
+                    return rc;
+                cur[br] = dst;
+            }
+            if ((rc = cast_rows(emb, 4, s->emb_bf16, 2, 1, d.hidden * 6, stream)) != AWA_OK)
+                return rc;
+            cur_emb = s->emb_bf16;
+            ping ^= 1;
+        }
+        if (s->profiling)
+            DIT_HIP(hipEventRecord(s->events[b], stream), "hipEventRecord");
+        const bool last = b == d.blocks - 1;
+        awa_dit_block* blk = last ? s->last : s->blocks[bf16][b % 2];
+        void* nv = last ? video_out : s->act[bf16][ping][0];
+        void* nt = last ? text_out : s->act[bf16][ping][1];
+        if ((rc = awa_dit_block_forward(blk, &video_weights[b], &text_weights[b], cur[0], cur[1], cur_emb, nv, nt,
+                                        stream)) != AWA_OK)
+            return rc;
+        cur[0] = nv;
+        cur[1] = nt;
+        ping ^= 1;
+    }
+    if (s->profiling)
+        DIT_HIP(hipEventRecord(s->events[d.blocks], stream), "hipEventRecord");
+    return AWA_OK;
+}
+
+int awa_dit_stack_block_times(const awa_dit_stack* s, float* block_ms)
+{
+    if (!s || !block_ms || !s->profiling)
+        return fail(AWA_ERR_INVALID, "profiling is not enabled");
+    for (int b = 0; b < s->desc.blocks; b++)
+        DIT_HIP(hipEventElapsedTime(&block_ms[b], s->events[b], s->events[b + 1]), "hipEventElapsedTime");
     return AWA_OK;
 }
 

@@ -93,3 +93,37 @@ def test_dit_block_rejects_bad_descriptions(gpu):
         args.update(kw)
         with pytest.raises(A.AwaError):
             A.DitBlock(**args)
+
+
+def test_dit_stack_matches_oracle_blocks(gpu):
+    """Four blocks with the precision switch after two (fp32, fp32, bf16,
+    bf16-last): the stack's outputs against the oracle block applied in turn,
+    with the carried video, text and embedding rounded to bf16 at the switch
+    (src/dit/dit_stack.cpp:934-950). The bf16 part is two blocks deep, so the
+    bf16 budget is taken per block: <= 2 * 2e-2."""
+    blocks, prefix = 4, 2
+    print("case dit stack 4 blocks, 2 fp32", flush=True)
+    rng = np.random.default_rng(77)
+    from test_dit_block_oracle import make_weights
+    g0, video, text, emb, _, _ = case(300, False)
+    ws = [(make_weights(rng), make_weights(rng)) for _ in range(blocks)]
+    stack = A.DitStack(*g0.args, g0.text_tokens, blocks, prefix, HEADS, HEAD_DIM, HIDDEN, MLP, EPS)
+    dev = [(DeviceBranch(wv, 4 if b < prefix else 2), DeviceBranch(wt, 4 if b < prefix else 2))
+           for b, (wv, wt) in enumerate(ws)]
+    bv, bt, be = upload_act(video, 4), upload_act(text, 4), upload_act(emb, 4)
+    ov, ot = A.DeviceBuffer(video.size * 2), A.DeviceBuffer(text.size * 2)
+    stack.run([d[0].struct for d in dev], [d[1].struct for d in dev], bv.ptr, bt.ptr, be.ptr, ov.ptr, ot.ptr)
+    A.synchronize()
+    got_v, got_t = download_act(ov, video.shape, 2), download_act(ot, text.shape, 2)
+    stack.destroy()
+    rv, rt, re = video, text, emb
+    for b in range(blocks):
+        g = geometry(g0.args + (g0.text_tokens,), b % 2 == 1)
+        bf16 = b >= prefix
+        if b == prefix:
+            rv, rt, re = O.round_bf16(rv), O.round_bf16(rt), O.round_bf16(re)
+        rv, rt = O.dit_block(g, rv, rt, re, ws[b][0], ws[b][1], HEADS, HEAD_DIM, EPS, b == blocks - 1, bf16=bf16)
+        rv, rt = rv.astype(np.float32), rt.astype(np.float32)
+    ev, et = rel(got_v, rv), rel(got_t, rt)
+    print(f"  rel err video {ev:.3g} text {et:.3g}", flush=True)
+    assert ev <= 4e-2 and et <= 4e-2
