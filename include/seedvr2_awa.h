@@ -283,7 +283,7 @@ typedef struct awa_dit_block_desc {
 typedef struct awa_dit_branch_weights {
     const void* qkv;            /* [3*heads*head_dim][hidden] */
     const void* proj_out;       /* [hidden][heads*head_dim] */
-    const float* proj_out_bias; /* [hidden] */
+    const float* proj_out_bias; /* [hidden], 16-byte aligned */
     const void* mlp_gate;       /* [mlp_hidden][hidden] (proj_in_gate) */
     const void* mlp_in;         /* [mlp_hidden][hidden] (proj_in) */
     const void* mlp_out;        /* [hidden][mlp_hidden] (proj_out) */

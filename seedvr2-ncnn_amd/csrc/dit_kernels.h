@@ -8,8 +8,14 @@
 namespace awa
 {
 
-// out = rmsnorm(in) * (emb scale + scale_b) + (emb shift + shift_b), per row
-// of `width`; shift_b = scale_b = null skips the modulation.
+// ada[r][c] = emb[c][r / 3][r % 3] + learned[r][c] for the 6 rows (attn
+// shift, scale, gate, mlp shift, scale, gate) of one branch: the Ada vectors
+// the row kernels below read.
+hipError_t launch_ada_prepare(const void* emb, int emb_elemsize, const float* learned, float* ada, int width,
+                              hipStream_t stream);
+
+// out = rmsnorm(in) * scale + shift, per row of `width`; scale = shift = null
+// skips the modulation.
 struct RowNormModulate
 {
     const void* in;
@@ -20,15 +26,11 @@ struct RowNormModulate
     long long out_stride;
     int rows, width;
     float eps;
-    const void* emb; // [width][2][3]
-    int emb_elemsize;
-    int layer;       // 0 attn, 1 mlp
-    const float* shift_b;
-    const float* scale_b;
+    const float* shift;
+    const float* scale;
 };
 
-// out = (h + bias) * (emb gate + gate_b) + residual (bias may be null;
-// gate_b = null takes the gate as 1).
+// out = (h + bias) * gate + residual (bias may be null; gate = null takes it as 1).
 struct GateResidual
 {
     const void* h;
@@ -42,10 +44,7 @@ struct GateResidual
     int out_elemsize;
     long long out_stride;
     int rows, width;
-    const void* emb;
-    int emb_elemsize;
-    int layer;
-    const float* gate_b;
+    const float* gate;
 };
 
 // out[:, c] = silu(in[:, c]) * in[:, width + c].

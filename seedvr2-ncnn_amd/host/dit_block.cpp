@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 #include <rocblas/rocblas.h>
 
+#include <cstdint>
 #include <cstring>
 #include <new>
 #include <string>
@@ -35,8 +36,10 @@ struct awa_dit_block
     int es = 4; // activation / GEMM element size
     int tokens[2] = {0, 0};
     // Workspace per branch: normalised input, QKV, attention output, GEMM
-    // output, post-attention residual, MLP hidden pair, SwiGLU output.
+    // output, post-attention residual, MLP hidden pair, SwiGLU output; and
+    // the branch's Ada vectors [6][hidden] fp32.
     void* ws[2][7] = {};
+    float* ada[2] = {nullptr, nullptr};
 };
 
 namespace
@@ -82,6 +85,12 @@ void release(awa_dit_block* b)
                 (void)hipFree(p);
             p = nullptr;
         }
+    for (float*& p : b->ada)
+    {
+        if (p)
+            (void)hipFree(p);
+        p = nullptr;
+    }
     if (b->blas)
         rocblas_destroy_handle(b->blas);
     b->blas = nullptr;
@@ -127,9 +136,16 @@ int gemm(awa_dit_block* b, const void* x, long long ldx, const void* w, void* y,
     return AWA_OK;
 }
 
+bool aligned16(const void* p)
+{
+    return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
 bool branch_weights_valid(const awa_dit_branch_weights* w, bool full)
 {
     if (!w || !w->qkv || !w->proj_out || !w->proj_out_bias || !w->norm_q || !w->norm_k)
+        return false;
+    if (!aligned16(w->proj_out_bias) || !aligned16(w->norm_q) || !aligned16(w->norm_k))
         return false;
     if (full && (!w->mlp_gate || !w->mlp_in || !w->mlp_out || !w->ada))
         return false;
@@ -147,8 +163,9 @@ int awa_dit_block_create(const awa_dit_block_desc* desc, awa_dit_block** out)
     *out = nullptr;
     if (desc->heads <= 0 || desc->head_dim != 128 || desc->hidden <= 0 || desc->mlp_hidden <= 0 ||
         (desc->precision != AWA_COMPUTE_F32 && desc->precision != AWA_COMPUTE_BF16) || !(desc->norm_eps >= 0.f) ||
-        desc->hidden % 8 || desc->mlp_hidden % 8)
-        return fail(AWA_ERR_INVALID, "invalid DiT block description (head_dim must be 128, widths multiples of 8)");
+        desc->hidden % 8 || desc->mlp_hidden % 8 || desc->hidden > 8192)
+        return fail(AWA_ERR_INVALID,
+                    "invalid DiT block description (head_dim must be 128, widths multiples of 8, hidden <= 8192)");
     awa_dit_block* b = new (std::nothrow) awa_dit_block;
     if (!b)
         return fail(AWA_ERR_ALLOC, "block allocation failed");
@@ -185,13 +202,15 @@ int awa_dit_block_create(const awa_dit_block_desc* desc, awa_dit_block** out)
         const long long M = b->tokens[br];
         const long long widths[7] = {desc->hidden, 3 * hd, hd, desc->hidden, desc->hidden, 2LL * desc->mlp_hidden,
                                      desc->mlp_hidden};
-        for (int k = 0; k < 7; k++)
-            if (hipMalloc(&b->ws[br][k], static_cast<size_t>(M * widths[k] * b->es)) != hipSuccess)
-            {
-                release(b);
-                delete b;
-                return fail(AWA_ERR_ALLOC, "DiT block workspace allocation failed");
-            }
+        bool ok = hipMalloc(&b->ada[br], static_cast<size_t>(6) * desc->hidden * sizeof(float)) == hipSuccess;
+        for (int k = 0; k < 7 && ok; k++)
+            ok = hipMalloc(&b->ws[br][k], static_cast<size_t>(M * widths[k] * b->es)) == hipSuccess;
+        if (!ok)
+        {
+            release(b);
+            delete b;
+            return fail(AWA_ERR_ALLOC, "DiT block workspace allocation failed");
+        }
     }
     *out = b;
     return AWA_OK;
@@ -214,7 +233,7 @@ int awa_dit_block_forward(awa_dit_block* b, const awa_dit_branch_weights* video_
     const awa_dit_block_desc& d = b->desc;
     const bool last = d.last_layer != 0;
     if (!branch_weights_valid(video_w, true) || !branch_weights_valid(text_w, !last))
-        return fail(AWA_ERR_INVALID, "missing DiT block weights");
+        return fail(AWA_ERR_INVALID, "missing DiT block weights (or bias / gammas not 16-byte aligned)");
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
     const int es = b->es;
     const int hidden = d.hidden;
@@ -225,11 +244,13 @@ int awa_dit_block_forward(awa_dit_block* b, const awa_dit_branch_weights* video_
     void* out[2] = {video_out, text_out};
     int rc;
 
-    // Attention half: norm + Ada in, QKV projection.
+    // Attention half: Ada vectors, norm + Ada in, QKV projection.
     for (int br = 0; br < 2; br++)
     {
         const int M = b->tokens[br];
         const bool modulate = br == 0 || !last;
+        if (modulate)
+            DIT_HIP(awa::launch_ada_prepare(emb, es, W[br]->ada, b->ada[br], hidden, stream), "ada_prepare launch");
         awa::RowNormModulate nm{};
         nm.in = in[br];
         nm.in_elemsize = es;
@@ -240,11 +261,8 @@ int awa_dit_block_forward(awa_dit_block* b, const awa_dit_branch_weights* video_
         nm.rows = M;
         nm.width = hidden;
         nm.eps = d.norm_eps;
-        nm.emb = emb;
-        nm.emb_elemsize = es;
-        nm.layer = 0;
-        nm.shift_b = modulate ? W[br]->ada + 0 * hidden : nullptr;
-        nm.scale_b = modulate ? W[br]->ada + 1 * hidden : nullptr;
+        nm.shift = modulate ? b->ada[br] + 0 * hidden : nullptr;
+        nm.scale = modulate ? b->ada[br] + 1 * hidden : nullptr;
         DIT_HIP(awa::launch_rmsnorm_modulate(nm, stream), "rmsnorm_modulate launch");
         if ((rc = gemm(b, b->ws[br][kNorm], hidden, W[br]->qkv, b->ws[br][kQkv], 3LL * hd, M, 3 * hd, hidden,
                        stream)) != AWA_OK)
@@ -281,10 +299,7 @@ int awa_dit_block_forward(awa_dit_block* b, const awa_dit_branch_weights* video_
         gr.out_stride = hidden;
         gr.rows = M;
         gr.width = hidden;
-        gr.emb = emb;
-        gr.emb_elemsize = es;
-        gr.layer = 0;
-        gr.gate_b = full ? W[br]->ada + 2 * hidden : nullptr;
+        gr.gate = full ? b->ada[br] + 2 * hidden : nullptr;
         DIT_HIP(awa::launch_gate_residual(gr, stream), "gate_residual launch");
         if (!full)
         {
@@ -303,11 +318,8 @@ int awa_dit_block_forward(awa_dit_block* b, const awa_dit_branch_weights* video_
         nm.rows = M;
         nm.width = hidden;
         nm.eps = d.norm_eps;
-        nm.emb = emb;
-        nm.emb_elemsize = es;
-        nm.layer = 1;
-        nm.shift_b = W[br]->ada + 3 * hidden;
-        nm.scale_b = W[br]->ada + 4 * hidden;
+        nm.shift = b->ada[br] + 3 * hidden;
+        nm.scale = b->ada[br] + 4 * hidden;
         DIT_HIP(awa::launch_rmsnorm_modulate(nm, stream), "rmsnorm_modulate launch");
         char* pair = static_cast<char*>(b->ws[br][kPair]);
         if ((rc = gemm(b, b->ws[br][kNorm], hidden, W[br]->mlp_gate, pair, 2LL * mh, M, mh, hidden, stream)) !=
@@ -341,10 +353,7 @@ int awa_dit_block_forward(awa_dit_block* b, const awa_dit_branch_weights* video_
         go.out_stride = hidden;
         go.rows = M;
         go.width = hidden;
-        go.emb = emb;
-        go.emb_elemsize = es;
-        go.layer = 1;
-        go.gate_b = W[br]->ada + 5 * hidden;
+        go.gate = b->ada[br] + 5 * hidden;
         DIT_HIP(awa::launch_gate_residual(go, stream), "gate_residual launch");
     }
     return AWA_OK;
