@@ -205,7 +205,7 @@ def dit_step(A, stream, steps: int, warmup: int = 2) -> dict:
         "bf16_block_ms": round(float(per_block[FP32_PREFIX:].mean()), 4),
         "steps": steps,
         "config": "32 blocks, hidden 2560, SwiGLU 6912, 20x128 heads, latent 9x16x16, windows 3x8x8, 64 text; "
-                  "blocks 0-8 fp32, 9-31 bf16; GEMMs on rocBLAS",
+                  "blocks 0-8 fp32, 9-31 bf16; GEMMs on hipBLASLt",
         "data": "random-init weights N(0, 0.02), inputs N(0, 1), synthetic",
     }
 

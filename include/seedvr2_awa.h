@@ -261,7 +261,8 @@ int awa_stack_block_flops(const awa_stack* stack, double* flops);
  * precision AWA_COMPUTE_F32: fp32 activations, GEMM weights and GEMMs (the
  * FP32 prefix blocks); AWA_COMPUTE_BF16: bf16 activations and GEMM weights,
  * fp32 accumulation and arithmetic (the BF16 blocks, dit_stack.cpp:519,
- * :550). The GEMMs are library GEMMs (rocBLAS). */
+ * :550). The GEMMs are library GEMMs (hipBLASLt). A block or stack object is
+ * used by one thread at a time (it caches GEMM descriptors on first use). */
 typedef struct awa_dit_block_desc {
     int source_t, source_h, source_w;    /* token grid */
     int windows_t, windows_h, windows_w; /* window counts (params 3/4/5) */

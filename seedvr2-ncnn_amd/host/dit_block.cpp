@@ -3,7 +3,7 @@
 // block, src/dit/dit_stack.cpp:951-963):
 //
 //   x_a   = rmsnorm(x) * (1 + ...) Ada "in" (attn)        rmsnorm_modulate kernel
-//   qkv   = x_a W_qkv^T                                    GEMM (rocBLAS)
+//   qkv   = x_a W_qkv^T                                    GEMM (hipBLASLt)
 //   att   = AWA(q/k RMSNorm(qkv))                          awa_forward_qknorm
 //   y     = (att W_out^T + b) * gate_attn + x              GEMM + gate_residual kernel
 //   x_m   = rmsnorm(y) Ada "in" (mlp)                      rmsnorm_modulate kernel
@@ -16,23 +16,35 @@
 // store activations and GEMM weights in bf16 (round to nearest even) and
 // accumulate in fp32. Parameter vectors (biases, gammas, Ada) are fp32.
 #include <hip/hip_runtime.h>
-#include <rocblas/rocblas.h>
+#include <hipblaslt/hipblaslt.h>
 
 #include <cstdint>
 #include <cstring>
+#include <map>
 #include <new>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "awa_internal.h"
 #include "dit_kernels.h"
 #include "seedvr2_awa.h"
 
+// One GEMM shape's hipBLASLt descriptors and the heuristic's first algorithm.
+struct GemmShape
+{
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
+    hipblasLtMatmulAlgo_t algo{};
+};
+
 struct awa_dit_block
 {
     awa_dit_block_desc desc{};
     awa_plan* plan = nullptr;
-    rocblas_handle blas = nullptr;
+    hipblasLtHandle_t lt = nullptr;
+    void* lt_workspace = nullptr;
+    std::map<std::tuple<int, int, int, long long, long long>, GemmShape> shapes;
     int es = 4; // activation / GEMM element size
     int tokens[2] = {0, 0};
     // Workspace per branch: normalised input, QKV, attention output, GEMM
@@ -91,9 +103,22 @@ void release(awa_dit_block* b)
             (void)hipFree(p);
         p = nullptr;
     }
-    if (b->blas)
-        rocblas_destroy_handle(b->blas);
-    b->blas = nullptr;
+    for (auto& kv : b->shapes)
+    {
+        GemmShape& g = kv.second;
+        for (hipblasLtMatrixLayout_t l : {g.a, g.b, g.c})
+            if (l)
+                hipblasLtMatrixLayoutDestroy(l);
+        if (g.desc)
+            hipblasLtMatmulDescDestroy(g.desc);
+    }
+    b->shapes.clear();
+    if (b->lt_workspace)
+        (void)hipFree(b->lt_workspace);
+    b->lt_workspace = nullptr;
+    if (b->lt)
+        hipblasLtDestroy(b->lt);
+    b->lt = nullptr;
     if (b->plan)
         awa_plan_destroy(b->plan);
     b->plan = nullptr;
@@ -115,24 +140,65 @@ awa_blob dense3(void* data, int w, int h, int c, int elemsize)
     return m;
 }
 
-// Y[M][N] (row stride ldy) = X[M][K] (row stride ldx) W[N][K]^T, fp32 accumulation.
+constexpr size_t kGemmWorkspace = 64u << 20;
+
+// Y[M][N] (row stride ldy) = X[M][K] (row stride ldx) W[N][K]^T, fp32
+// accumulation. Column-major view: Y^T (N x M, ld ldy) = op(A) B with A = W
+// stored K x N (ld K) and transposed, B = X^T (K x M, ld ldx). The
+// descriptors and the heuristic's algorithm are built once per shape.
 int gemm(awa_dit_block* b, const void* x, long long ldx, const void* w, void* y, long long ldy, int M, int N, int K,
          hipStream_t stream)
 {
     if (M <= 0)
         return AWA_OK;
-    if (rocblas_set_stream(b->blas, stream) != rocblas_status_success)
-        return fail(AWA_ERR_DEVICE, "rocblas_set_stream failed");
+    const auto key = std::make_tuple(M, N, K, ldx, ldy);
+    auto it = b->shapes.find(key);
+    if (it == b->shapes.end())
+    {
+        GemmShape g;
+        const hipDataType t = b->es == 2 ? HIP_R_16BF : HIP_R_32F;
+        const hipblasOperation_t opT = HIPBLAS_OP_T, opN = HIPBLAS_OP_N;
+        bool ok = hipblasLtMatmulDescCreate(&g.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
+                  hipblasLtMatmulDescSetAttribute(g.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opT, sizeof(opT)) ==
+                      HIPBLAS_STATUS_SUCCESS &&
+                  hipblasLtMatmulDescSetAttribute(g.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN, sizeof(opN)) ==
+                      HIPBLAS_STATUS_SUCCESS &&
+                  hipblasLtMatrixLayoutCreate(&g.a, t, K, N, K) == HIPBLAS_STATUS_SUCCESS &&
+                  hipblasLtMatrixLayoutCreate(&g.b, t, K, M, ldx) == HIPBLAS_STATUS_SUCCESS &&
+                  hipblasLtMatrixLayoutCreate(&g.c, t, N, M, ldy) == HIPBLAS_STATUS_SUCCESS;
+        hipblasLtMatmulPreference_t pref = nullptr;
+        hipblasLtMatmulHeuristicResult_t result{};
+        int found = 0;
+        if (ok)
+        {
+            const uint64_t ws = kGemmWorkspace;
+            ok = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
+                 hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
+                                                       sizeof(ws)) == HIPBLAS_STATUS_SUCCESS &&
+                 hipblasLtMatmulAlgoGetHeuristic(b->lt, g.desc, g.a, g.b, g.c, g.c, pref, 1, &result, &found) ==
+                     HIPBLAS_STATUS_SUCCESS &&
+                 found > 0 && result.workspaceSize <= kGemmWorkspace;
+        }
+        if (pref)
+            hipblasLtMatmulPreferenceDestroy(pref);
+        if (!ok)
+        {
+            for (hipblasLtMatrixLayout_t l : {g.a, g.b, g.c})
+                if (l)
+                    hipblasLtMatrixLayoutDestroy(l);
+            if (g.desc)
+                hipblasLtMatmulDescDestroy(g.desc);
+            return fail(AWA_ERR_DEVICE, "hipBLASLt has no algorithm for a GEMM of the block");
+        }
+        g.algo = result.algo;
+        it = b->shapes.emplace(key, g).first;
+    }
     const float alpha = 1.f, beta = 0.f;
-    const rocblas_datatype t = b->es == 2 ? rocblas_datatype_bf16_r : rocblas_datatype_f32_r;
-    // Column-major view: Y^T (N x M, ld ldy) = W (N x K from the K x N
-    // column-major W^T, transposed) * X^T (K x M, ld ldx).
-    const rocblas_status st =
-        rocblas_gemm_ex(b->blas, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &alpha, w, t, K, x, t,
-                        static_cast<rocblas_int>(ldx), &beta, y, t, static_cast<rocblas_int>(ldy), y, t,
-                        static_cast<rocblas_int>(ldy), rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-    if (st != rocblas_status_success)
-        return fail(AWA_ERR_DEVICE, std::string("rocblas_gemm_ex failed: ") + rocblas_status_to_string(st));
+    const GemmShape& g = it->second;
+    const hipblasStatus_t st = hipblasLtMatmul(b->lt, g.desc, &alpha, w, g.a, x, g.b, &beta, y, g.c, y, g.c, &g.algo,
+                                               b->lt_workspace, kGemmWorkspace, stream);
+    if (st != HIPBLAS_STATUS_SUCCESS)
+        return fail(AWA_ERR_DEVICE, "hipblasLtMatmul failed");
     return AWA_OK;
 }
 
@@ -188,11 +254,11 @@ int awa_dit_block_create(const awa_dit_block_desc* desc, awa_dit_block** out)
         delete b;
         return rc;
     }
-    if (rocblas_create_handle(&b->blas) != rocblas_status_success)
+    if (hipblasLtCreate(&b->lt) != HIPBLAS_STATUS_SUCCESS || hipMalloc(&b->lt_workspace, kGemmWorkspace) != hipSuccess)
     {
         release(b);
         delete b;
-        return fail(AWA_ERR_DEVICE, "rocblas_create_handle failed");
+        return fail(AWA_ERR_DEVICE, "hipBLASLt handle or workspace creation failed");
     }
     b->tokens[0] = desc->source_t * desc->source_h * desc->source_w;
     b->tokens[1] = desc->text_tokens;
