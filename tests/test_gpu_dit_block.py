@@ -127,3 +127,39 @@ def test_dit_stack_matches_oracle_blocks(gpu):
     ev, et = rel(got_v, rv), rel(got_t, rt)
     print(f"  rel err video {ev:.3g} text {et:.3g}", flush=True)
     assert ev <= 4e-2 and et <= 4e-2
+
+
+@pytest.mark.parametrize("precision,shifted", [(A.COMPUTE_F32, False), (A.COMPUTE_BF16, True)])
+def test_dit_block_benchmark_shape(gpu, precision, shifted):
+    """One block at the benchmark workload: latent 9x16x16, windows 3x8x8,
+    64 text tokens, hidden 2560 = 20 x 128, SwiGLU 6912; weights N(0, 0.02)
+    (the random init of the benchmark), inputs N(0, 1). Same tolerances."""
+    bf16 = precision == A.COMPUTE_BF16
+    print(f"case dit block benchmark shape bf16={bf16} shifted={shifted}", flush=True)
+    heads, hidden, mlp = 20, 2560, 6912
+    g = geometry((9, 16, 16, 3, 8, 8, 64), shifted)
+    rng = np.random.default_rng(2026 + bf16)
+    n = lambda *s, sd=0.02: (rng.standard_normal(s) * sd).astype(np.float32)
+
+    def weights():
+        return O.DitBranchWeights(qkv=n(3 * hidden, hidden), proj_out=n(hidden, hidden), proj_out_bias=n(hidden),
+                                  mlp_gate=n(mlp, hidden), mlp_in=n(mlp, hidden), mlp_out=n(hidden, mlp),
+                                  norm_q=rng.uniform(0.5, 1.5, HEAD_DIM).astype(np.float32),
+                                  norm_k=rng.uniform(0.5, 1.5, HEAD_DIM).astype(np.float32), ada=n(6, hidden, sd=0.5))
+
+    wv, wt = weights(), weights()
+    video, text, emb = n(g.source_tokens, hidden, sd=1.0), n(g.text_tokens, hidden, sd=1.0), n(hidden * 6, sd=1.0)
+    es = 2 if bf16 else 4
+    blk = A.DitBlock(*g.args, g.text_tokens, g.shifted, heads, HEAD_DIM, hidden, mlp, False, precision, EPS)
+    dv, dt = DeviceBranch(wv, es), DeviceBranch(wt, es)
+    bv, bt, be = upload_act(video, es), upload_act(text, es), upload_act(emb, es)
+    ov, ot = A.DeviceBuffer(video.size * es), A.DeviceBuffer(text.size * es)
+    blk.forward(dv.struct, dt.struct, bv.ptr, bt.ptr, be.ptr, ov.ptr, ot.ptr)
+    A.synchronize()
+    got_v, got_t = download_act(ov, video.shape, es), download_act(ot, text.shape, es)
+    blk.destroy()
+    ref_v, ref_t = O.dit_block(g, video, text, emb, wv, wt, heads, HEAD_DIM, EPS, False, bf16=bf16)
+    ev, et = rel(got_v, ref_v), rel(got_t, ref_t)
+    print(f"  rel err video {ev:.3g} text {et:.3g}", flush=True)
+    tol = 2e-2 if bf16 else 1e-5
+    assert ev <= tol and et <= tol
