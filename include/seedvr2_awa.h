@@ -187,6 +187,12 @@ int awa_forward_qknorm(const awa_plan* plan, const awa_blob* video_qkv, const aw
  * a pairwise tree), so results match the CPU oracle bit for bit. */
 int awa_rmsnorm(const awa_blob* input, const float* gamma, float eps, const awa_blob* output, void* stream);
 
+/* DitQKVConcat::forward (src/dit/dit_precision.cpp:95-137, dit_qkv_concat.comp):
+ * q, k (fp32) and v (fp32 or bf16), each a dims-3 Mat(d, H, N), into one fp32
+ * Mat(d, 3H, N) = [token][q heads, k heads, v heads][d]; v is promoted exactly.
+ * The AWA input of a BF16 block (fp32 Q/K from the q/k RMSNorm, bf16 V). */
+int awa_qkv_concat(const awa_blob* q, const awa_blob* k, const awa_blob* v, const awa_blob* output, void* stream);
+
 /* SeedVR2AWAPack (src/awa/awa_layers.cpp:419-458, :501-578): packed = Mat(d, 3H, S)
  * fp32, cu_seqlens = Mat(nwin+1) fp32. */
 int awa_pack(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv, const awa_blob* packed,

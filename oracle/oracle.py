@@ -222,6 +222,22 @@ def rmsnorm(x: np.ndarray, gamma, eps: float) -> np.ndarray:
     return out
 
 
+def qkv_concat(q: np.ndarray, k: np.ndarray, v: np.ndarray) -> np.ndarray:
+    """DitQKVConcat (src/dit/shader/dit_qkv_concat.comp:17-31): q, k, v of
+    shape [tokens][heads][d] into [tokens][3 heads][d] fp32; output row y
+    reads head y % heads of q (y < heads), k (y < 2 heads) or v, whose values
+    are promoted exactly."""
+    q, k, v = (np.asarray(a, np.float32) for a in (q, k, v))
+    if q.ndim != 3 or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("q, k and v must be [tokens][heads][d] of one shape")
+    tokens, heads, d = q.shape
+    out = np.empty((tokens, 3 * heads, d), np.float32)
+    for y in range(3 * heads):
+        src = q if y < heads else (k if y < 2 * heads else v)
+        out[:, y, :] = src[:, y % heads, :]
+    return out
+
+
 def qk_norm_inputs(video: np.ndarray, text: np.ndarray, gammas, eps: float):
     """The DiT block's q/k RMSNorm on raw QKV: video [N][3][H][d], text
     [T_x][3][H][d]; gammas (q_video, k_video, q_text, k_text) of head_dim each.

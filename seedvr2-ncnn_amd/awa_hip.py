@@ -34,7 +34,7 @@ EXPORTED_SYMBOLS = (
     "awa_event_synchronize", "awa_event_elapsed_ms", "awa_fill_normal", "awa_fill_normal_scaled", "awa_plan_create", "awa_plan_destroy",
     "awa_plan_info_get", "awa_plan_windows", "awa_plan_sequence_index", "awa_plan_cu_seqlens",
     "awa_plan_video_positions", "awa_plan_text_positions", "awa_plan_rope_table", "awa_plan_upload",
-    "awa_qkv_shape", "awa_forward", "awa_forward_qknorm", "awa_rmsnorm", "awa_pack", "awa_mmrope",
+    "awa_qkv_shape", "awa_forward", "awa_forward_qknorm", "awa_rmsnorm", "awa_qkv_concat", "awa_pack", "awa_mmrope",
     "awa_window_attention", "awa_unpack", "awa_cast",
     "awa_stack_create", "awa_stack_destroy", "awa_stack_run", "awa_stack_set_profiling", "awa_stack_set_graph", "awa_stack_block_times",
     "awa_stack_block_flops", "awa_dit_block_create", "awa_dit_block_destroy", "awa_dit_block_forward",
@@ -150,6 +150,7 @@ def lib() -> ctypes.CDLL:
         L.awa_forward.argtypes = [vp, bp, bp, bp, bp, i, vp]
         L.awa_forward_qknorm.argtypes = [vp, bp, bp, ctypes.POINTER(AwaQkNorm), bp, bp, i, vp]
         L.awa_rmsnorm.argtypes = [bp, vp, ctypes.c_float, bp, vp]
+        L.awa_qkv_concat.argtypes = [bp, bp, bp, bp, vp]
         L.awa_pack.argtypes = [vp, bp, bp, bp, bp, vp]
         L.awa_mmrope.argtypes = [vp, bp, bp, vp]
         L.awa_window_attention.argtypes = [vp, bp, bp, i, vp]
@@ -534,6 +535,12 @@ class AttentionStack:
 
 def rmsnorm(inp: AwaBlob, gamma_ptr: Optional[int], eps: float, out: AwaBlob, stream: Optional[Stream] = None) -> None:
     check(lib().awa_rmsnorm(ctypes.byref(inp), gamma_ptr, eps, ctypes.byref(out), _s(stream)), "awa_rmsnorm")
+
+
+def qkv_concat(q: AwaBlob, k: AwaBlob, v: AwaBlob, out: AwaBlob, stream: Optional[Stream] = None) -> None:
+    """DitQKVConcat: fp32 q, k and fp32/bf16 v, each Mat(d, H, N), into fp32 Mat(d, 3H, N)."""
+    check(lib().awa_qkv_concat(ctypes.byref(q), ctypes.byref(k), ctypes.byref(v), ctypes.byref(out), _s(stream)),
+          "awa_qkv_concat")
 
 
 def cast(inp: AwaBlob, out: AwaBlob, stream: Optional[Stream] = None) -> None:

@@ -914,6 +914,29 @@ int awa_rmsnorm(const awa_blob* input, const float* gamma, float eps, const awa_
     return AWA_OK;
 }
 
+int awa_qkv_concat(const awa_blob* q, const awa_blob* k, const awa_blob* v, const awa_blob* output, void* stream)
+{
+    // DitQKVConcat::forward (src/dit/dit_precision.cpp:114-137): three dims-3
+    // Mats of one shape (w = head_dim, h = heads, c = tokens), q and k fp32, v
+    // fp32 or bf16; output Mat(w, 3h, c) fp32.
+    if (!q || !k || !v || !output || !q->data || !k->data || !v->data || !output->data)
+        return fail(AWA_ERR_INVALID, "null blob");
+    for (const awa_blob* b : {q, k, v})
+        if (b->dims != 3 || b->n != 1 || b->w != q->w || b->h != q->h || b->c != q->c || b->w <= 0 || b->h <= 0 ||
+            b->c <= 0 || b->cstep < static_cast<long long>(b->w) * b->h)
+            return fail(AWA_ERR_INVALID, "qkv concat inputs must be dims-3 Mats of one shape");
+    if (q->elemsize != 4 || k->elemsize != 4 || (v->elemsize != 2 && v->elemsize != 4))
+        return fail(AWA_ERR_INVALID, "qkv concat takes fp32 q and k, fp32 or bf16 v");
+    if (output->dims != 3 || output->n != 1 || output->w != q->w || output->h != 3 * q->h || output->c != q->c ||
+        output->elemsize != 4 || output->cstep < 3ll * q->w * q->h)
+        return fail(AWA_ERR_INVALID, "qkv concat output must be an fp32 Mat(w, 3h, c)");
+    HIP_TRY(awa::launch_qkv_concat(static_cast<const float*>(q->data), q->cstep, static_cast<const float*>(k->data),
+                                   k->cstep, v->data, v->elemsize, v->cstep, static_cast<float*>(output->data),
+                                   output->cstep, q->w, q->h, q->c, as_stream(stream)),
+            "qkv concat kernel launch");
+    return AWA_OK;
+}
+
 int awa_cast(const awa_blob* input, const awa_blob* output, void* stream)
 {
     if (!input || !output || !input->data || !output->data)

@@ -114,6 +114,12 @@ hipError_t launch_rmsnorm(const void* in, int in_elemsize, long long in_cstep, v
 hipError_t launch_cast(const void* in, int in_elemsize, void* out, int out_elemsize, const CastShape& s,
                        hipStream_t stream);
 
+// DitQKVConcat: out[token][3 heads][width] (fp32) from q, k (fp32) and v
+// (fp32 or bf16), each [token][heads][width] with its own token step.
+hipError_t launch_qkv_concat(const float* q, long long q_cstep, const float* k, long long k_cstep, const void* v,
+                             int v_elemsize, long long v_cstep, float* out, long long out_cstep, int width, int heads,
+                             int tokens, hipStream_t stream);
+
 hipError_t launch_fill_normal(void* dst, size_t count, int elemsize, unsigned long long seed, float stddev,
                               hipStream_t stream);
 hipError_t launch_zero(void* dst, size_t bytes, hipStream_t stream);

@@ -329,6 +329,52 @@ __global__ void cast_kernel(const void* in, int in_elemsize, void* out, int out_
     store_elem(out, b * s.out_nstep + c * s.out_cstep + inner, out_elemsize, v);
 }
 
+// ---- DitQKVConcat: out[token][y][x] = q / k / v[token][y % heads][x] for y in
+// [0, heads) / [heads, 2 heads) / [2 heads, 3 heads); v fp32 or bf16 (exact
+// promotion), out fp32. One thread per 4 consecutive x when every row is
+// 16-byte aligned, else per element. ----
+__global__ void qkv_concat_kernel(const float* q, long long q_cstep, const float* k, long long k_cstep,
+                                  const void* v, int v_elemsize, long long v_cstep, float* out, long long out_cstep,
+                                  int width, int heads, int tokens, int vec)
+{
+    const int groups = width / vec;
+    const long long per_token = 3ll * heads * groups;
+    const long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= per_token * tokens)
+        return;
+    const long long token = idx / per_token;
+    const int rem = static_cast<int>(idx - token * per_token);
+    const int y = rem / groups;
+    const int x = (rem - y * groups) * vec;
+    const int head = y % heads;
+    const long long i = static_cast<long long>(head) * width + x;
+    float* dst = out + token * out_cstep + static_cast<long long>(y) * width + x;
+    if (vec == 4)
+    {
+        float4 val;
+        if (y < heads)
+            val = *reinterpret_cast<const float4*>(q + token * q_cstep + i);
+        else if (y < 2 * heads)
+            val = *reinterpret_cast<const float4*>(k + token * k_cstep + i);
+        else if (v_elemsize == 4)
+            val = *reinterpret_cast<const float4*>(static_cast<const float*>(v) + token * v_cstep + i);
+        else
+        {
+            const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(v) + token * v_cstep + i);
+            val = make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                              __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u));
+        }
+        *reinterpret_cast<float4*>(dst) = val;
+        return;
+    }
+    if (y < heads)
+        *dst = q[token * q_cstep + i];
+    else if (y < 2 * heads)
+        *dst = k[token * k_cstep + i];
+    else
+        *dst = load_elem(v, token * v_cstep + i, v_elemsize);
+}
+
 // ---- Seeded N(0,1): splitmix64 counter hash -> two 32-bit uniforms -> Box-Muller ----
 __device__ __forceinline__ uint64_t splitmix64(uint64_t x)
 {
@@ -469,6 +515,24 @@ hipError_t launch_rmsnorm(const void* in, int in_elemsize, long long in_cstep, v
         return hipSuccess;
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows, channels), dim3(128), 0, stream, in, in_elemsize, in_cstep, out,
                        out_elemsize, out_cstep, width, gamma, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_qkv_concat(const float* q, long long q_cstep, const float* k, long long k_cstep, const void* v,
+                             int v_elemsize, long long v_cstep, float* out, long long out_cstep, int width, int heads,
+                             int tokens, hipStream_t stream)
+{
+    if (width <= 0 || heads <= 0 || tokens <= 0)
+        return hipSuccess;
+    const bool aligned = width % 4 == 0 && q_cstep % 4 == 0 && k_cstep % 4 == 0 && v_cstep % 4 == 0 &&
+                         out_cstep % 4 == 0 && reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(v) % (4 * v_elemsize) == 0 &&
+                         reinterpret_cast<uintptr_t>(out) % 16 == 0;
+    const int vec = aligned ? 4 : 1;
+    const long long total = 3ll * heads * (width / vec) * tokens;
+    hipLaunchKernelGGL(qkv_concat_kernel, dim3(grid_for(total)), dim3(kBlock), 0, stream, q, q_cstep, k, k_cstep, v,
+                       v_elemsize, v_cstep, out, out_cstep, width, heads, tokens, vec);
     return hipGetLastError();
 }
 

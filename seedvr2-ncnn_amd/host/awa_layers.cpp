@@ -116,6 +116,18 @@ int Mat::create(int w_, size_t elemsize_, Allocator* allocator)
     return allocate(allocator);
 }
 
+int Mat::create(int w_, int h_, size_t elemsize_, Allocator* allocator)
+{
+    release();
+    dims = 2;
+    w = w_;
+    h = h_;
+    d = c = n = 1;
+    elemsize = elemsize_;
+    cstep = nstep = static_cast<long long>(w_) * h_;
+    return allocate(allocator);
+}
+
 int Mat::create(int w_, int h_, int c_, size_t elemsize_, Allocator* allocator, int n_)
 {
     release();
@@ -416,6 +428,7 @@ int Net::load_param_mem(const char* text)
         for (size_t i = 4 + nb + nt; i < f.size(); i++)
             if (l.pd.load_field(f[i]) != 0)
                 return fail_load("invalid parameter " + f[i] + " in layer " + l.name);
+        l.featmask = l.pd.get(31, 0);
         for (const std::string& top : l.tops)
             if (!produced.emplace(top, 1).second)
                 return fail_load("blob " + top + " produced twice");

@@ -82,8 +82,9 @@ public:
     bool empty() const { return data == nullptr || total() == 0; }
     long long total() const { return nstep * n; }
 
-    // dims 1: Mat(w); dims 3: Mat(w, h, c); dims 4: Mat(w, h, d, c); n > 1 adds batches.
+    // dims 1: Mat(w); dims 2: Mat(w, h); dims 3: Mat(w, h, c); dims 4: Mat(w, h, d, c); n > 1 adds batches.
     int create(int w, size_t elemsize, Allocator* allocator);
+    int create(int w, int h, size_t elemsize, Allocator* allocator);
     int create(int w, int h, int c, size_t elemsize, Allocator* allocator, int n = 1);
     int create_4d(int w, int h, int d, int c, size_t elemsize, Allocator* allocator, int n = 1);
     void release();
@@ -154,6 +155,7 @@ struct ParamLayer
     std::vector<std::string> bottoms, tops;
     ParamDict pd;
     std::unique_ptr<Layer> layer; // registered types only; other types are recorded, not run
+    int featmask = 0;             // ncnn Layer::featmask (param 31); bit 2 keeps a layer's storage fp32
 };
 
 // Custom-layer registry with ncnn::Net's register_custom_layer signature, and
@@ -176,6 +178,7 @@ public:
     int load_param(const char* path);
     int load_param_mem(const char* text);
     const std::vector<ParamLayer>& layers() const { return layers_; }
+    std::vector<ParamLayer>& mutable_layers() { return layers_; }
     const ParamLayer* find_layer(const std::string& name) const;
     int blob_count() const { return blob_count_; }
     const std::string& last_error() const { return error_; }

@@ -12,6 +12,14 @@
 //       Seeded inputs on device 0, the four-layer chain and the fused chain;
 //       writes inputs and outputs as float32 files into OUTDIR and prints the
 //       largest staged-vs-fused difference.
+//   awa_layers_check dit
+//       Host-only checks of the DiT precision layers (DitRMSNorm,
+//       DitQKVConcat): registration, params, and
+//       configure_dit_block_precision_layers on paired and last-block graphs.
+//   awa_layers_check ditforward OUTDIR tokens heads bf16
+//       Seeded raw q/k/v on device 0 through RMSNorm (q, k; affine) and the
+//       QKV concat as a BF16 (bf16 = 1) or FP32 block runs them; writes the
+//       inputs, gammas and output as float32 files into OUTDIR.
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -20,6 +28,7 @@
 #include <vector>
 
 #include "awa_layers.h"
+#include "dit_layers.h"
 
 using seedvr2::hip::Mat;
 using seedvr2::hip::Net;
@@ -307,6 +316,207 @@ int run_forward(int argc, char** argv)
     return 0;
 }
 
+// A DiT block graph in the export's shape, reduced to what the precision
+// configuration reads: per modulated branch an Ada parameter (MemoryData
+// constant_p_ada_*), a Split into its six vectors and six BinaryOp sums with
+// the embedding; five Gemms and a Swish per branch with an MLP, two Gemms
+// for the last block's text branch; residual BinaryOps that read no
+// parameter; the AWA Pack.
+std::string dit_graph(bool last_block, int extra_sums)
+{
+    std::vector<std::string> lines;
+    int blobs = 0;
+    auto add = [&](const std::string& line, int tops) {
+        lines.push_back(line);
+        blobs += tops;
+    };
+    add("Input in_video 0 1 video", 1);
+    add("Input in_text 0 1 text", 1);
+    add("Input in_emb 0 1 emb", 1);
+    add("Split split_emb 1 6 emb e0 e1 e2 e3 e4 e5", 6);
+    for (const char* br : {"vid", "txt"})
+    {
+        const std::string b = br;
+        const bool modulated = !last_block || b == "vid";
+        if (modulated)
+        {
+            add("MemoryData constant_p_ada_" + b + " 0 1 ada_" + b + " 0=2560 1=6", 1);
+            add("Reshape view_ada_" + b + " 1 1 ada_" + b + " adar_" + b + " 0=2560 1=6", 1);
+            std::string split = "Split split_ada_" + b + " 1 6 adar_" + b;
+            for (int i = 0; i < 6; i++)
+                split += " a" + b + std::to_string(i);
+            add(split, 6);
+            for (int i = 0; i < 6; i++)
+                add("BinaryOp sum_" + b + std::to_string(i) + " 2 1 e" + std::to_string(i) + " a" + b +
+                        std::to_string(i) + " s" + b + std::to_string(i) + " 0=0",
+                    1);
+        }
+        add("Gemm qkv_" + b + " 1 1 " + (b == "vid" ? "video" : "text") + " qkv_" + b, 1);
+        add("Gemm proj_" + b + " 1 1 att_" + b + " proj_" + b, 1);
+        add("BinaryOp resid_" + b + " 2 1 proj_" + b + " " + (b == "vid" ? "video" : "text") + " y_" + b + " 0=0",
+            1);
+        if (modulated)
+        {
+            add("Gemm gate_" + b + " 1 1 y_" + b + " g_" + b, 1);
+            add("Gemm in_" + b + " 1 1 y_" + b + " i_" + b, 1);
+            add("Swish swish_" + b + " 1 1 g_" + b + " sw_" + b, 1);
+            add("Gemm out_" + b + " 1 1 sw_" + b + " o_" + b, 1);
+        }
+    }
+    add("SeedVR2AWAPack awa_pack 2 2 qkv_vid qkv_txt packed cu 0=9 1=16 2=16 3=3 4=8 5=8 6=64 7=0", 2);
+    add("SeedVR2AWAUnpack awa_unpack 1 2 packed att_vid att_txt 0=9 1=16 2=16 3=3 4=8 5=8 6=64 7=0", 2);
+    for (int i = 0; i < extra_sums; i++)
+        add("BinaryOp extra_sum" + std::to_string(i) + " 2 1 e0 avid0 x" + std::to_string(i) + " 0=0", 1);
+    std::string text = "7767517\n" + std::to_string(lines.size()) + " " + std::to_string(blobs) + "\n";
+    for (const std::string& l : lines)
+        text += l + "\n";
+    return text;
+}
+
+int run_dit()
+{
+    Net net;
+    seedvr2::register_dit_block_precision_layers(net);
+    const auto types = net.custom_layer_types();
+    expect(types.size() == 2 && types[0] == "Concat" && types[1] == "RMSNorm", "RMSNorm and Concat registered");
+
+    auto norm = net.create_custom_layer("RMSNorm");
+    ParamDict pd;
+    pd.set(0, 128);
+    pd.set(1, 1e-5f);
+    expect(norm && norm->load_param(pd) == 0, "RMSNorm load_param");
+    auto* rms = static_cast<DitRMSNorm*>(norm.get());
+    expect(rms->affine_size == 128 && rms->eps == 1e-5f && rms->affine == 1, "RMSNorm params 0-2 and defaults");
+    Option opt;
+    expect(rms->upload_model(opt) != 0, "RMSNorm affine without gamma is rejected");
+    std::vector<Mat> tops;
+    expect(rms->forward({Mat()}, tops, opt) != 0, "RMSNorm forward before upload is rejected");
+    ParamDict bad;
+    expect(net.create_custom_layer("RMSNorm")->load_param(bad) != 0, "RMSNorm without affine_size is rejected");
+
+    auto concat = net.create_custom_layer("Concat");
+    expect(concat && concat->load_param(ParamDict()) == 0 && concat->create_pipeline(opt) != 0,
+           "Concat on axis 0 is rejected at create_pipeline");
+    ParamDict axis1;
+    axis1.set(0, 1);
+    expect(concat->load_param(axis1) == 0 && concat->create_pipeline(opt) == 0, "Concat on axis 1");
+    expect(concat->forward({Mat(), Mat()}, tops, opt) != 0, "Concat needs three inputs");
+
+    struct Case
+    {
+        bool last;
+        int extra;
+        bool ok;
+        int sums, gemms, swishes;
+    };
+    for (const Case& c : {Case{false, 0, true, 12, 10, 2}, Case{true, 0, true, 6, 7, 1}, Case{false, 1, false, 13, 10, 2},
+                          Case{true, 6, false, 12, 7, 1}})
+    {
+        Net g;
+        seedvr2::register_dit_block_precision_layers(g);
+        const std::string text = dit_graph(c.last, c.extra);
+        if (g.load_param_mem(text.c_str()) != 0)
+        {
+            std::printf("FAIL graph load: %s\n", g.last_error().c_str());
+            failures++;
+            continue;
+        }
+        seedvr2::DitBlockPrecision found;
+        const bool ok = seedvr2::configure_dit_block_precision_layers(g, &found);
+        char what[160];
+        std::snprintf(what, sizeof what, "configure last=%d extra=%d: %s (sums %d gemms %d swishes %d)", c.last,
+                      c.extra, ok ? "accepted" : "rejected", found.sums, found.gemms, found.swishes);
+        expect(ok == c.ok && found.sums == c.sums && found.gemms == c.gemms && found.swishes == c.swishes, what);
+        const auto* pack = g.find_layer("awa_pack");
+        const auto* view = g.find_layer("view_ada_vid");
+        const auto* split = g.find_layer("split_ada_vid");
+        const auto* emb_split = g.find_layer("split_emb");
+        expect(pack && (pack->featmask & 4) && view && (view->featmask & 4) && split && (split->featmask & 4) &&
+                   emb_split && emb_split->featmask == 0,
+               "featmask bit 2 on the Pack and the Ada views only");
+        bool residual_fp32 = false;
+        for (const std::string& name : found.fp32_sums)
+            residual_fp32 = residual_fp32 || name.rfind("resid_", 0) == 0;
+        expect(!residual_fp32, "residual sums keep the block's storage");
+    }
+    std::printf("dit: %s\n", failures ? "FAILED" : "all passed");
+    return failures ? 1 : 0;
+}
+
+int run_dit_forward(int argc, char** argv)
+{
+    if (argc < 6)
+    {
+        std::fprintf(stderr, "usage: ditforward OUTDIR tokens heads bf16\n");
+        return 2;
+    }
+    const std::string dir = argv[2];
+    const int tokens = std::atoi(argv[3]), heads = std::atoi(argv[4]), d = 128;
+    const bool bf16 = std::atoi(argv[5]) != 0;
+    const size_t es = bf16 ? 2 : 4;
+    if (awa_runtime_init(0) != AWA_OK)
+    {
+        std::fprintf(stderr, "no device: %s\n", awa_last_error());
+        return 1;
+    }
+    Option opt;
+    opt.use_bf16_storage = bf16;
+    Net net;
+    seedvr2::register_dit_block_precision_layers(net);
+    ParamDict pn;
+    pn.set(0, d);
+    pn.set(1, 1e-5f);
+    ParamDict pc;
+    pc.set(0, 1);
+    auto norm_q = net.create_custom_layer("RMSNorm");
+    auto norm_k = net.create_custom_layer("RMSNorm");
+    auto concat = net.create_custom_layer("Concat");
+    int seed = 0;
+    for (auto* layer : {norm_q.get(), norm_k.get()})
+    {
+        auto* rms = static_cast<DitRMSNorm*>(layer);
+        if (rms->load_param(pn) != 0 || rms->gamma_data.create(d, 4, nullptr) != 0)
+            return 1;
+        awa_fill_normal(rms->gamma_data.data, d, 4, 20261000ULL + seed++, nullptr);
+        if (rms->upload_model(opt) != 0 || rms->create_pipeline(opt) != 0)
+            return 1;
+    }
+    if (concat->load_param(pc) != 0 || concat->create_pipeline(opt) != 0)
+        return 1;
+    // Raw projections Mat(d, H, tokens) in the block's storage type.
+    Mat q, k, v;
+    for (Mat* m : {&q, &k, &v})
+    {
+        if (m->create(d, heads, tokens, es, nullptr) != 0)
+            return 1;
+        awa_fill_normal(m->data, static_cast<size_t>(m->total()), static_cast<int>(es), 20261010ULL + seed++, nullptr);
+    }
+    std::vector<Mat> nq, nk, qkv;
+    int rc = norm_q->forward({q}, nq, opt);
+    if (rc == 0)
+        rc = norm_k->forward({k}, nk, opt);
+    if (rc == 0)
+        rc = concat->forward({nq[0], nk[0], v}, qkv, opt);
+    if (rc != 0 || awa_stream_synchronize(nullptr) != 0)
+    {
+        std::fprintf(stderr, "dit forward failed rc=%d: %s\n", rc, awa_last_error());
+        return 1;
+    }
+    const bool shapes = nq[0].elemsize == 4 && qkv[0].dims == 3 && qkv[0].w == d && qkv[0].h == 3 * heads &&
+                        qkv[0].c == tokens && qkv[0].elemsize == 4;
+    if (!shapes || !write_file(dir + "/q.f32", to_host_float(q)) || !write_file(dir + "/k.f32", to_host_float(k)) ||
+        !write_file(dir + "/v.f32", to_host_float(v)) ||
+        !write_file(dir + "/gamma_q.f32", to_host_float(static_cast<DitRMSNorm*>(norm_q.get())->gamma_data)) ||
+        !write_file(dir + "/gamma_k.f32", to_host_float(static_cast<DitRMSNorm*>(norm_k.get())->gamma_data)) ||
+        !write_file(dir + "/qkv.f32", to_host_float(qkv[0])))
+    {
+        std::fprintf(stderr, "bad output shape or cannot write into %s\n", dir.c_str());
+        return 1;
+    }
+    std::printf("ditforward: qkv %dx%dx%d fp32 written\n", qkv[0].w, qkv[0].h, qkv[0].c);
+    return 0;
+}
+
 } // namespace
 
 int main(int argc, char** argv)
@@ -317,7 +527,12 @@ int main(int argc, char** argv)
         return run_forward(argc, argv);
     if (argc >= 2 && std::strcmp(argv[1], "param") == 0)
         return run_param();
-    std::fprintf(stderr, "usage: %s params | param | forward OUTDIR t h w nt nh nw text shifted heads bf16\n",
+    if (argc >= 2 && std::strcmp(argv[1], "dit") == 0)
+        return run_dit();
+    if (argc >= 2 && std::strcmp(argv[1], "ditforward") == 0)
+        return run_dit_forward(argc, argv);
+    std::fprintf(stderr, "usage: %s params | param | dit | forward OUTDIR t h w nt nh nw text shifted heads bf16 | "
+                 "ditforward OUTDIR tokens heads bf16\n",
                  argv[0]);
     return 2;
 }

@@ -180,3 +180,36 @@ def test_qknorm_invalid_arguments(gpu):
     neg = A.AwaQkNorm(dg.bufs[0].ptr, dg.bufs[1].ptr, dg.bufs[2].ptr, dg.bufs[3].ptr, -1.0)
     with pytest.raises(RuntimeError):
         plan.forward_qknorm(vq.blob, tq.blob, neg, vo.blob, to.blob, A.COMPUTE_F32)
+
+
+@pytest.mark.parametrize("v_elemsize", [4, 2])
+@pytest.mark.parametrize("width,heads,tokens", [(128, 20, 37), (6, 3, 11)])
+def test_qkv_concat_bit_exact(gpu, v_elemsize, width, heads, tokens):
+    """DitQKVConcat (awa_qkv_concat) against the oracle, bit for bit: the
+    16-byte path (width 128) and the per-element path (width 6)."""
+    print(f"case qkv concat v_elem={v_elemsize} width={width} heads={heads} tokens={tokens}", flush=True)
+    rng = np.random.RandomState(width + heads + v_elemsize)
+    q, k, v = (rng.randn(tokens, heads, width).astype(np.float32) for _ in range(3))
+    if v_elemsize == 2:
+        v = bf16_round(v)
+    mats = []
+    for x, es in ((q, 4), (k, 4), (v, v_elemsize)):
+        m = mat3(width, heads, tokens, es)
+        upload_mat3(m, x)
+        mats.append(m)
+    out = mat3(width, 3 * heads, tokens, 4)
+    A.qkv_concat(mats[0].blob, mats[1].blob, mats[2].blob, out.blob)
+    A.synchronize()
+    np.testing.assert_array_equal(read_mat3(out), O.qkv_concat(q, k, v))
+
+
+def test_qkv_concat_rejects_bad_blobs(gpu):
+    q, k = mat3(128, 4, 8, 4), mat3(128, 4, 8, 4)
+    out = mat3(128, 12, 8, 4)
+    for v in (mat3(128, 4, 7, 4), mat3(128, 5, 8, 4)):
+        with pytest.raises(A.AwaError):
+            A.qkv_concat(q.blob, k.blob, v.blob, out.blob)
+    with pytest.raises(A.AwaError):  # q must be fp32
+        A.qkv_concat(mat3(128, 4, 8, 2).blob, k.blob, mat3(128, 4, 8, 2).blob, out.blob)
+    with pytest.raises(A.AwaError):  # output must be Mat(w, 3h, c)
+        A.qkv_concat(q.blob, k.blob, mat3(128, 4, 8, 2).blob, mat3(128, 8, 8, 4).blob)

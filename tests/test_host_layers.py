@@ -1,7 +1,8 @@
 """The C++ layer surface (SeedVR2AWAPack / SeedVR2MMRoPE /
-SeedVR2WindowAttention / SeedVR2AWAUnpack over the C ABI), driven by
+SeedVR2WindowAttention / SeedVR2AWAUnpack over the C ABI, and the DiT
+precision layers DitRMSNorm / DitQKVConcat on the AWA input), driven by
 tests/cpp/awa_layers_check the way a host of the reference's ncnn layers
-drives them (src/awa/awa_layers.h:47-223)."""
+drives them (src/awa/awa_layers.h:47-223, src/dit/dit_precision.cpp:22-343)."""
 
 from __future__ import annotations
 
@@ -92,3 +93,36 @@ def test_shape_trace(gpu, tmp_path):
                "unpack.video.out", "unpack.text.out", "forward.video.in"):
         assert op in ops, op
     assert "awa-trace op=pack.video.in dims=3 w=128 h=6 d=1 c=256 elemsize=4 pack=1" in lines
+
+
+def test_dit_precision_layers():
+    """DitRMSNorm / DitQKVConcat registration and params, and
+    configure_dit_block_precision_layers on paired and last-block graphs
+    (src/dit/dit_precision.cpp:284-343): the Ada parameter views get
+    featmask bit 2, the parameter sums are counted, wrong counts reject."""
+    r = run_check("dit")
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "dit: all passed" in r.stdout
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bf16", [0, 1])
+def test_dit_precision_layer_chain_bit_exact(gpu, tmp_path, bf16):
+    """RMSNorm(q), RMSNorm(k) (affine, fp32 out) and the QKV concat through
+    the layer surface as an FP32 or BF16 block runs them, against the
+    oracle's rmsnorm and qkv_concat: bit for bit (the norm follows the
+    shader's summation order; the concat moves and promotes exactly)."""
+    tokens, heads, d = 45, 5, 128
+    print(f"dit precision chain tokens={tokens} heads={heads} bf16={bf16}", flush=True)
+    r = run_check("ditforward", str(tmp_path), str(tokens), str(heads), str(bf16))
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+    def load(name, shape):
+        return np.fromfile(os.path.join(tmp_path, name), np.float32).reshape(shape)
+
+    q, k, v = (load(f"{x}.f32", (tokens, heads, d)) for x in "qkv")
+    gq, gk = load("gamma_q.f32", (d,)), load("gamma_k.f32", (d,))
+    want = O.qkv_concat(O.rmsnorm(q, gq, 1e-5), O.rmsnorm(k, gk, 1e-5), v)
+    np.testing.assert_array_equal(load("qkv.f32", (tokens, 3 * heads, d)), want)

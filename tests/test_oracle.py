@@ -574,3 +574,18 @@ def test_qk_norm_inputs_normalises_q_and_k_only():
     for src, dst, gq, gk in ((video, v, gammas[0], gammas[1]), (text, t, gammas[2], gammas[3])):
         assert np.allclose(dst[:, 0], _rms_f64(src[:, 0], gq, 1e-5), rtol=1e-5, atol=1e-6)
         assert np.allclose(dst[:, 1], _rms_f64(src[:, 1], gk, 1e-5), rtol=1e-5, atol=1e-6)
+
+
+def test_qkv_concat_is_the_qkv_interleave():
+    """DitQKVConcat against numpy's concatenation along the head axis (an
+    independent formulation), with distinct values per (tensor, token, head,
+    feature); a planted head mapping y // 3 instead of y % heads is rejected."""
+    tokens, heads, d = 5, 3, 6
+    base = np.arange(tokens * heads * d, dtype=np.float32).reshape(tokens, heads, d)
+    q, k, v = base, base + 1000.0, base + 2000.0
+    got = O.qkv_concat(q, k, v)
+    assert np.array_equal(got, np.concatenate([q, k, v], axis=1))
+    planted = np.stack([(q, k, v)[y // heads][:, y // 3] for y in range(3 * heads)], axis=1)
+    assert not np.array_equal(got, planted)
+    with pytest.raises(ValueError):
+        O.qkv_concat(q, k, v[:, :2])
