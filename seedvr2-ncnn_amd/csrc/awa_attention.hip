@@ -134,24 +134,10 @@ __device__ __forceinline__ void rope_pair_fma(float& x0, float& x1, float c, flo
     x1 = fmaf(b, c, a * s);
 }
 
-// Row table entry of window-local row i: video rows store their local
-// (t, h, w) in 10-bit fields, text rows set bit 31 and store k.
-__device__ __forceinline__ uint32_t encode_row(const WindowDesc& win, int i)
-{
-    if (i < win.video_tokens)
-    {
-        const int area = win.eh * win.ew;
-        const int lt = i / area;
-        const int rem = i - lt * area;
-        const int lh = rem / win.ew;
-        const int lw = rem - lh * win.ew;
-        return (static_cast<uint32_t>(lt) << 20) | (static_cast<uint32_t>(lh) << 10) | static_cast<uint32_t>(lw);
-    }
-    return 0x80000000u | static_cast<uint32_t>(i - win.video_tokens);
-}
-
-// A decoded row table entry. Both interpretations are computed and selected,
-// so rows of a wave that mix video and text take no divergent branch.
+// Window-local row i of a window, decoded: video rows (i < video_tokens)
+// are in (t, h, w) order inside the window box, text rows follow. Both
+// interpretations are computed and selected, so rows of a wave that mix
+// video and text take no divergent branch.
 struct RowRef
 {
     bool text;
@@ -161,19 +147,40 @@ struct RowRef
     uint32_t token; // video token index (meaningful for video rows)
 };
 
-__device__ __forceinline__ RowRef decode_row(uint32_t e, int t0, int h0, int w0, int text_tokens, int source_h,
-                                             int source_w)
+// Reciprocals of the window's h*w and w extents, for quotients of row
+// indices: floor(i / d) = int((i + 0.5) * fl(1 / d)) exactly, since the
+// relative error of the product (a few fp32 ulps) times i / d stays below
+// the distance 0.5 / d of (i + 0.5) / d from an integer for any i < 2^20.
+struct RowDivisors
+{
+    float inv_area, inv_ew;
+    int area, ew;
+};
+
+__device__ __forceinline__ RowDivisors row_divisors(const WindowDesc& win)
+{
+    RowDivisors d;
+    d.area = win.eh * win.ew;
+    d.ew = win.ew;
+    d.inv_area = 1.f / static_cast<float>(d.area);
+    d.inv_ew = 1.f / static_cast<float>(d.ew);
+    return d;
+}
+
+__device__ __forceinline__ RowRef window_row(const WindowDesc& win, const RowDivisors& dv, int i, int text_tokens,
+                                             int source_h, int source_w)
 {
     RowRef r;
-    const int k = static_cast<int>(e & 0x7fffffffu);
-    const int lt = static_cast<int>((e >> 20) & 1023u);
-    const int lh = static_cast<int>((e >> 10) & 1023u);
-    const int lw = static_cast<int>(e & 1023u);
-    r.text = (e & 0x80000000u) != 0;
+    const int lt = static_cast<int>((static_cast<float>(i) + 0.5f) * dv.inv_area);
+    const int rem = i - lt * dv.area;
+    const int lh = static_cast<int>((static_cast<float>(rem) + 0.5f) * dv.inv_ew);
+    const int lw = rem - lh * dv.ew;
+    const int k = i - win.video_tokens;
+    r.text = k >= 0;
     r.k = k;
-    r.t = t0 + lt;
-    r.h = h0 + lh;
-    r.w = w0 + lw;
+    r.t = win.t0 + lt;
+    r.h = win.h0 + lh;
+    r.w = win.w0 + lw;
     // Unsigned arithmetic: for text rows the video fields are meaningless
     // (and may wrap), the value is then never used.
     r.token = (static_cast<uint32_t>(r.t) * static_cast<uint32_t>(source_h) + static_cast<uint32_t>(r.h)) *
@@ -332,19 +339,19 @@ __global__ __launch_bounds__(VARIANT == kVariantWidePipe ? 512 : 256,
     const long long packed_qkv = static_cast<long long>(p.heads) * kHeadDim;
     const float scale_log2 = p.scale_log2;
 
-    // Element pointer of (window row i < L, qkv, head) in its source blob.
+    const RowDivisors divisors = row_divisors(win);
+    auto decode = [&](int i) { return window_row(win, divisors, i, p.text_tokens, p.source_h, p.source_w); };
+    // Element pointer of (decoded window row, qkv, head) in its source blob.
+    auto source_ptr = [&](const RowRef& r, int qkv) -> const TIn* {
+        return r.text ? text_base + r.k * t_tok + qkv * t_qkv + head_off
+                      : video_base + static_cast<long long>(r.token) * v_tok + qkv * v_qkv + head_off;
+    };
+    // Element pointer of (window row i < L, qkv, head).
     auto row_ptr = [&](int i, int qkv) -> const TIn* {
         if constexpr (FUSED)
-        {
-            const RowRef r =
-                decode_row(encode_row(win, i), win.t0, win.h0, win.w0, p.text_tokens, p.source_h, p.source_w);
-            return r.text ? text_base + r.k * t_tok + qkv * t_qkv + head_off
-                          : video_base + static_cast<long long>(r.token) * v_tok + qkv * v_qkv + head_off;
-        }
+            return source_ptr(decode(i), qkv);
         else
-        {
             return packed_base + (win.seq_start + i) * packed_row + qkv * packed_qkv + head_off;
-        }
     };
 
     // RoPE table: its loads are issued first and land in LDS after the Q
@@ -393,14 +400,20 @@ __global__ __launch_bounds__(VARIANT == kVariantWidePipe ? 512 : 256,
     for (int i = tid; i < tiles * KT; i += kThreads)
     {
         const int src = min(i, L - 1);
-        row_k[i] = reinterpret_cast<const unsigned char*>(row_ptr(src, 1)) - load_base;
-        row_v[i] = reinterpret_cast<const unsigned char*>(row_ptr(src, 2)) - load_base;
         if constexpr (FUSED)
         {
-            const RowRef r =
-                decode_row(encode_row(win, src), win.t0, win.h0, win.w0, p.text_tokens, p.source_h, p.source_w);
+            // One decode per row: V sits one qkv step after K.
+            const RowRef r = decode(src);
+            const TIn* const k_ptr = source_ptr(r, 1);
+            row_k[i] = reinterpret_cast<const unsigned char*>(k_ptr) - load_base;
+            row_v[i] = reinterpret_cast<const unsigned char*>(k_ptr + (r.text ? t_qkv : v_qkv)) - load_base;
             row_code[i] = static_cast<uint32_t>(r.ct) | (static_cast<uint32_t>(r.ch) << 8) |
                           (static_cast<uint32_t>(r.cw) << 16) | (static_cast<uint32_t>(p.rope_coords) << 24);
+        }
+        else
+        {
+            row_k[i] = reinterpret_cast<const unsigned char*>(row_ptr(src, 1)) - load_base;
+            row_v[i] = reinterpret_cast<const unsigned char*>(row_ptr(src, 2)) - load_base;
         }
     }
     __syncthreads();
@@ -985,8 +998,7 @@ __global__ __launch_bounds__(VARIANT == kVariantWidePipe ? 512 : 256,
     // ---- store: lane holds features db*32 + 8*g + 4*half + [0,4) ----
     if constexpr (FUSED)
     {
-        const RowRef r =
-            decode_row(encode_row(win, qi), win.t0, win.h0, win.w0, p.text_tokens, p.source_h, p.source_w);
+        const RowRef r = decode(qi);
         if (!r.text)
         {
             TOut* dst = static_cast<TOut*>(p.video_out.data) + r.t * p.video_out.ts + r.h * p.video_out.hs +
