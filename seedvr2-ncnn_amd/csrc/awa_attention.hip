@@ -273,6 +273,8 @@ __host__ __device__ inline int rope_table_bytes(bool fused, int rope_coords)
 //   kVariantNarrow: 4 waves (128 query rows), single-buffered K/V tiles of 64
 //     (bf16) or 32 (fp32) keys, two barriers per tile; the LDS footprint stays
 //     under half a CU's, so that two workgroups share a CU.
+//   kVariantWide: the same loop on 8 waves (256 query rows): a unit of up to
+//     256 rows stages and rotates its K/V tiles once.
 //   kVariantWidePipe: 8 waves (256 query rows), double-buffered tiles and a
 //     software pipeline with one barrier per tile: the scores of tile t+1 and
 //     the PV of tile t are issued next to the softmax of tile t and the
@@ -280,12 +282,12 @@ __host__ __device__ inline int rope_table_bytes(bool fused, int rope_coords)
 // NORM (fused mode): the DiT block's q/k RMSNorm over head_dim is applied to
 // Q and K rows as they are gathered, before RoPE.
 template <typename TIn, typename TOut, bool BF16, bool FUSED, int VARIANT, bool NORM>
-__global__ __launch_bounds__(VARIANT == kVariantWidePipe ? 512 : 256,
-                             VARIANT == kVariantWidePipe ? 1 : 2) void window_attention_kernel(const AttentionLaunch p)
+__global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
+                             VARIANT != kVariantNarrow ? 1 : 2) void window_attention_kernel(const AttentionLaunch p)
 {
     static_assert(!NORM || FUSED, "the q/k RMSNorm is fused into the gather");
-    constexpr bool WIDE = VARIANT == kVariantWidePipe;
-    constexpr bool PIPE = WIDE;
+    constexpr bool WIDE = VARIANT != kVariantNarrow;
+    constexpr bool PIPE = VARIANT == kVariantWidePipe;
     constexpr int kThreads = WIDE ? 512 : 256;
     constexpr int kQueryRows = kThreads / 2; // 32 rows per wave
     static_assert(kQueryRows == (WIDE ? awa::kWideQueryRows : awa::kQueryRows), "work items match the variant");
@@ -1035,7 +1037,7 @@ static hipError_t launch_one(const AttentionLaunch& p, hipStream_t stream)
     const size_t row_table = static_cast<size_t>((p.max_window_tokens + 63) & ~63) * (2 * sizeof(long long) + 4);
     const size_t dynamic_lds = kNormLdsBytes<NORM> + rope_table_bytes(FUSED, p.rope_coords) + row_table;
     hipLaunchKernelGGL((window_attention_kernel<TIn, TOut, BF16, FUSED, VARIANT, NORM>), dim3(p.work_count),
-                       dim3(VARIANT == kVariantWidePipe ? 512 : 256), dynamic_lds, stream, p);
+                       dim3(VARIANT != kVariantNarrow ? 512 : 256), dynamic_lds, stream, p);
     return hipGetLastError();
 }
 
@@ -1062,12 +1064,20 @@ hipError_t launch_attention(const AttentionLaunch& p, hipStream_t stream)
 {
     if (p.work_count <= 0)
         return hipSuccess;
-    // Instantiated: bf16 MFMA in the narrow variant, fp32 MFMA in the 8-wave
-    // pipelined one; the fused q/k RMSNorm in fused mode only.
+    // Instantiated: bf16 MFMA in the narrow and the 8-wave single-buffered
+    // variants, fp32 MFMA in the 8-wave pipelined one; the fused q/k RMSNorm
+    // in fused mode only.
     if (p.qk_norm && !p.fused)
         return hipErrorInvalidValue;
     if (p.bf16_mfma)
     {
+        if (p.variant == kVariantWide)
+        {
+            if (!p.fused)
+                return launch_typed<true, false, kVariantWide>(p, stream);
+            return p.qk_norm ? launch_typed<true, true, kVariantWide, true>(p, stream)
+                             : launch_typed<true, true, kVariantWide>(p, stream);
+        }
         if (p.variant != kVariantNarrow)
             return hipErrorInvalidValue;
         if (!p.fused)

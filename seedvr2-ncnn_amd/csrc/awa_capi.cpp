@@ -167,13 +167,26 @@ int check_plan_uploaded(const awa_plan* plan)
 // their K/V reads.
 constexpr int kXcds = 8;
 
-// Attention kernel variant per arithmetic: fp32 MFMA takes the 8-wave
-// pipeline (one workgroup per unit of up to 256 rows, its long MFMA tiles
-// hide the softmax and the staging), bf16 MFMA the 4-wave kernel (two
-// workgroups per CU).
-int attention_variant(bool bf16_mfma)
+// Attention kernel variant per arithmetic and geometry. fp32 MFMA takes the
+// 8-wave pipeline (one workgroup per unit of up to 256 rows; its long MFMA
+// tiles hide the softmax and the staging). bf16 MFMA takes the 8-wave
+// single-buffered kernel when its 256-row query blocks leave no more waves
+// idle than 128-row blocks would (each unit's K/V tiles are then staged and
+// rotated once instead of once per 128-row block), else the 4-wave kernel
+// with two workgroups per CU.
+int attention_variant(bool bf16_mfma, const awa_plan& plan)
 {
-    return bf16_mfma ? awa::kVariantNarrow : awa::kVariantWidePipe;
+    if (!bf16_mfma)
+        return awa::kVariantWidePipe;
+    long long idle_wide = 0, idle_narrow = 0;
+    for (const awa::WindowDesc& w : plan.window_descs)
+    {
+        const int L = w.video_tokens + plan.text_tokens;
+        const int waves = (L + 31) / 32;
+        idle_wide += (L + awa::kWideQueryRows - 1) / awa::kWideQueryRows * (awa::kWideQueryRows / 32) - waves;
+        idle_narrow += (L + awa::kQueryRows - 1) / awa::kQueryRows * (awa::kQueryRows / 32) - waves;
+    }
+    return idle_wide <= idle_narrow ? awa::kVariantWide : awa::kVariantNarrow;
 }
 
 std::vector<awa::WorkItem> build_work(const awa_plan& plan, int heads, int rows_per_block)
@@ -704,9 +717,9 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
         p.norm_eps = norm->eps;
     }
     p.windows = plan->dev.windows;
-    p.variant = attention_variant(p.bf16_mfma);
-    p.work = p.variant == awa::kVariantWidePipe ? plan->work_wide : plan->work;
-    p.work_count = p.variant == awa::kVariantWidePipe ? plan->work_wide_count : plan->work_count;
+    p.variant = attention_variant(p.bf16_mfma, *plan);
+    p.work = p.variant != awa::kVariantNarrow ? plan->work_wide : plan->work;
+    p.work_count = p.variant != awa::kVariantNarrow ? plan->work_wide_count : plan->work_count;
     p.rope_cs = plan->dev.rope_cs;
     p.rope_coords = plan->rope_coords;
     p.max_window_tokens = plan->max_window_tokens;
@@ -839,9 +852,9 @@ int awa_window_attention(const awa_plan* plan, const awa_blob* input, const awa_
     p.packed_out_row = output->cstep;
     p.windows = plan->dev.windows;
     // Same variant choice as the fused layer, so that both give the same bits.
-    p.variant = attention_variant(p.bf16_mfma);
-    p.work = p.variant == awa::kVariantWidePipe ? plan->work_wide : plan->work;
-    p.work_count = p.variant == awa::kVariantWidePipe ? plan->work_wide_count : plan->work_count;
+    p.variant = attention_variant(p.bf16_mfma, *plan);
+    p.work = p.variant != awa::kVariantNarrow ? plan->work_wide : plan->work;
+    p.work_count = p.variant != awa::kVariantNarrow ? plan->work_wide_count : plan->work_count;
     p.max_window_tokens = plan->max_window_tokens;
     p.heads = heads;
     p.text_tokens = plan->text_tokens;

@@ -17,6 +17,7 @@ constexpr int kWideQueryRows = 256; // query rows per workgroup of the wide vari
 // Attention kernel variants.
 constexpr int kVariantNarrow = 0;   // 4 waves, single-buffered tiles
 constexpr int kVariantWidePipe = 1; // 8 waves, double-buffered, software-pipelined
+constexpr int kVariantWide = 2;     // 8 waves, single-buffered tiles (the narrow loop on 256 rows)
 constexpr int kMaxRopeCoords = 128; // RoPE coordinates the fused kernel holds in LDS
 constexpr int kMaxFusedWindowTokens = 1536; // rows of the fused kernel's LDS row table
 
