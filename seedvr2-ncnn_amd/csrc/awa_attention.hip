@@ -814,16 +814,12 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
                 for (int i = 0; i < 16; i++)
                     negm[i] = -row_max;
             }
-            float psum = 0.f;
+            // The row sum is taken in pv(), over the bf16 probabilities.
 #pragma unroll
             for (int b = 0; b < kBlocks; b++)
 #pragma unroll
                 for (int i = 0; i < 16; i++)
-                {
                     s[b][i] = __builtin_amdgcn_exp2f(s[b][i]);
-                    psum += s[b][i];
-                }
-            row_sum += psum;
             return;
         }
         if (!decltype(lazy)::value || __any(tile_max > row_max + kRescaleThreshold))
@@ -863,6 +859,21 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
                     pb[2 * b][e] = static_cast<__bf16>(s[b][e]);
                     pb[2 * b + 1][e] = static_cast<__bf16>(s[b][8 + e]);
                 }
+            if constexpr (kRel)
+            {
+                // Row sum over the probabilities as the MFMA sees them (bf16):
+                // one dot product with (1, 1) per pair, so that numerator and
+                // denominator share the rounding.
+                const bf16x2 ones = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
+#pragma unroll
+                for (int j = 0; j < 2 * kBlocks; j++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                    {
+                        const bf16x2 pair = {pb[j][2 * q], pb[j][2 * q + 1]};
+                        row_sum = __builtin_amdgcn_fdot2_f32_bf16(pair, ones, row_sum, false);
+                    }
+            }
             // The four output chains are interleaved: consecutive MFMAs are
             // independent. With d = 32 db + col (col < 32), 8 vt_swizzle(d)
             // = 16 db + 8 (col / 16), so the swizzled column (8 half + 16 j)

@@ -153,12 +153,16 @@ __global__ void unpack_text_kernel(const int* text_positions, int window_count, 
 
 // ---- Fused-path text mean over the per-window partials [nwin][T_x][H][d]
 // (fp32 or bf16, the layer's output type) ----
-// One thread per output element pair; the window loop is unrolled so that 8
-// loads per thread are in flight, and the sum keeps window order.
+// One thread per output element pair. Windows are read in batches of 16
+// unconditional loads (indices past the last window are clamped to it and
+// their values replaced by zero), so that a layer of up to 16 windows waits
+// for one memory latency; the sum keeps window order (adding +0 leaves every
+// partial sum unchanged).
 template <typename TPart>
 __global__ void text_mean_kernel(const TPart* partials, int window_count, int text_tokens, int row_elems,
                                  void* out, long long out_row, int out_elemsize)
 {
+    constexpr int kBatch = 16;
     const int pairs = row_elems / 2;
     const long long total = static_cast<long long>(text_tokens) * pairs;
     const long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -179,25 +183,20 @@ __global__ void text_mean_kernel(const TPart* partials, int window_count, int te
         }
     };
     float sx = 0.f, sy = 0.f;
-    int w = 0;
-    for (; w + 8 <= window_count; w += 8)
+    const int last = window_count - 1;
+    for (int w = 0; w < window_count; w += kBatch)
     {
-        float2 v[8];
+        float2 v[kBatch];
 #pragma unroll
-        for (int j = 0; j < 8; j++)
-            v[j] = load_pair(w + j);
+        for (int j = 0; j < kBatch; j++)
+            v[j] = load_pair(min(w + j, last));
 #pragma unroll
-        for (int j = 0; j < 8; j++)
+        for (int j = 0; j < kBatch; j++)
         {
-            sx += v[j].x;
-            sy += v[j].y;
+            const bool valid = w + j < window_count;
+            sx += valid ? v[j].x : 0.f;
+            sy += valid ? v[j].y : 0.f;
         }
-    }
-    for (; w < window_count; w++)
-    {
-        const float2 v = load_pair(w);
-        sx += v.x;
-        sy += v.y;
     }
     const float n = static_cast<float>(window_count);
     const long long o = k * out_row + e;
