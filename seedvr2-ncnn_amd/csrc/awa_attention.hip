@@ -317,7 +317,6 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
         return;
     const WindowDesc win = item.win;
     const int head = item.head;
-    const int qblock = item.qblock;
     const int L = win.video_tokens + p.text_tokens;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -371,10 +370,12 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
         }
     }
 
-    const int wave_row0 = qblock * kQueryRows + wave * 32;
-    const bool wave_active = wave_row0 < L;
+    const int wave_row0 = item.row0 + wave * 32;
+    // Waves past the item's rows only stage; their rows (if any) belong to
+    // another work item and are neither computed nor stored here.
+    const bool wave_active = wave * 32 < item.rows && wave_row0 < L;
     const int qi = wave_row0 + col;
-    const bool q_valid = qi < L;
+    const bool q_valid = wave_active && qi < L;
     const int q_row = min(qi, L - 1);
 
     // Q rows go straight to registers; their addresses do not need the table.

@@ -189,20 +189,31 @@ int attention_variant(bool bf16_mfma, const awa_plan& plan)
     return idle_wide <= idle_narrow ? awa::kVariantWide : awa::kVariantNarrow;
 }
 
+// Query rows of a (window, head) unit of L rows as work items of at most
+// rows_per_block rows (multiples of 32): (first row, rows).
+std::vector<std::pair<int, int>> split_rows(int L, int rows_per_block)
+{
+    std::vector<std::pair<int, int>> items;
+    for (int r = 0; r < L; r += rows_per_block)
+        items.push_back({r, std::min(rows_per_block, (L - r + 31) / 32 * 32)});
+    return items;
+}
+
 std::vector<awa::WorkItem> build_work(const awa_plan& plan, int heads, int rows_per_block)
 {
     struct Unit
     {
         long long cost;
-        int window, head, qblocks;
+        int window, head;
+        std::vector<std::pair<int, int>> items;
     };
     std::vector<Unit> units;
     for (size_t w = 0; w < plan.window_descs.size(); w++)
     {
         const int L = plan.window_descs[w].video_tokens + plan.text_tokens;
-        const int qblocks = (L + rows_per_block - 1) / rows_per_block;
+        const auto items = split_rows(L, rows_per_block);
         for (int h = 0; h < heads; h++)
-            units.push_back({static_cast<long long>(L) * L, static_cast<int>(w), h, qblocks});
+            units.push_back({static_cast<long long>(L) * L, static_cast<int>(w), h, items});
     }
     std::stable_sort(units.begin(), units.end(), [](const Unit& a, const Unit& b) { return a.cost > b.cost; });
     std::vector<std::vector<awa::WorkItem>> lists(kXcds);
@@ -211,8 +222,8 @@ std::vector<awa::WorkItem> build_work(const awa_plan& plan, int heads, int rows_
     {
         const int x = static_cast<int>(std::min_element(load.begin(), load.end()) - load.begin());
         load[x] += u.cost;
-        for (int q = 0; q < u.qblocks; q++)
-            lists[x].push_back({plan.window_descs[u.window], u.window, u.head, q, 0});
+        for (const auto& it : u.items)
+            lists[x].push_back({plan.window_descs[u.window], u.window, u.head, it.first, it.second});
     }
     size_t longest = 0;
     for (const auto& l : lists)

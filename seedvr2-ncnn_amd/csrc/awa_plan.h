@@ -30,14 +30,16 @@ struct alignas(16) WindowDesc
 
 // One workgroup's share of the fused / packed attention: the window (its
 // descriptor is embedded so that a workgroup needs a single dependent load to
-// start), the head and the query block. window < 0 marks padding.
+// start), the head and the query rows [row0, row0 + rows) of the window,
+// rows a multiple of 32 and at most the variant's rows per workgroup.
+// window < 0 marks padding.
 struct alignas(16) WorkItem
 {
     WindowDesc win;
     int window;
     int head;
-    int qblock;
-    int reserved;
+    int row0;
+    int rows;
 };
 
 // Packed-row descriptor for the staged kernels: source row (video index, or
