@@ -30,7 +30,8 @@
 #include "dit_kernels.h"
 #include "seedvr2_awa.h"
 
-// One GEMM shape's hipBLASLt descriptors and the heuristic's first algorithm.
+// One GEMM shape's hipBLASLt descriptors and its algorithm: the fastest of
+// the heuristic's candidates, timed on first use.
 struct GemmShape
 {
     hipblasLtMatmulDesc_t desc = nullptr;
@@ -141,11 +142,17 @@ awa_blob dense3(void* data, int w, int h, int c, int elemsize)
 }
 
 constexpr size_t kGemmWorkspace = 64u << 20;
+constexpr int kGemmCandidates = 16;
+constexpr int kGemmTimedRuns = 3;
 
 // Y[M][N] (row stride ldy) = X[M][K] (row stride ldx) W[N][K]^T, fp32
 // accumulation. Column-major view: Y^T (N x M, ld ldy) = op(A) B with A = W
 // stored K x N (ld K) and transposed, B = X^T (K x M, ld ldx). The
-// descriptors and the heuristic's algorithm are built once per shape.
+// descriptors are built once per shape, and the algorithm is chosen then:
+// up to kGemmCandidates of the heuristic's algorithms each run once to warm
+// up and kGemmTimedRuns times under HIP events on the call's own operands
+// (y is rewritten by the call that follows), and the fastest is kept. A
+// stream under graph capture takes the heuristic's first algorithm.
 int gemm(awa_dit_block* b, const void* x, long long ldx, const void* w, void* y, long long ldy, int M, int N, int K,
          hipStream_t stream)
 {
@@ -167,7 +174,7 @@ int gemm(awa_dit_block* b, const void* x, long long ldx, const void* w, void* y,
                   hipblasLtMatrixLayoutCreate(&g.b, t, K, M, ldx) == HIPBLAS_STATUS_SUCCESS &&
                   hipblasLtMatrixLayoutCreate(&g.c, t, N, M, ldy) == HIPBLAS_STATUS_SUCCESS;
         hipblasLtMatmulPreference_t pref = nullptr;
-        hipblasLtMatmulHeuristicResult_t result{};
+        hipblasLtMatmulHeuristicResult_t results[kGemmCandidates] = {};
         int found = 0;
         if (ok)
         {
@@ -175,12 +182,56 @@ int gemm(awa_dit_block* b, const void* x, long long ldx, const void* w, void* y,
             ok = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
                  hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
                                                        sizeof(ws)) == HIPBLAS_STATUS_SUCCESS &&
-                 hipblasLtMatmulAlgoGetHeuristic(b->lt, g.desc, g.a, g.b, g.c, g.c, pref, 1, &result, &found) ==
-                     HIPBLAS_STATUS_SUCCESS &&
-                 found > 0 && result.workspaceSize <= kGemmWorkspace;
+                 hipblasLtMatmulAlgoGetHeuristic(b->lt, g.desc, g.a, g.b, g.c, g.c, pref, kGemmCandidates, results,
+                                                 &found) == HIPBLAS_STATUS_SUCCESS &&
+                 found > 0 && results[0].workspaceSize <= kGemmWorkspace;
         }
         if (pref)
             hipblasLtMatmulPreferenceDestroy(pref);
+        if (ok)
+        {
+            g.algo = results[0].algo;
+            hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+            (void)hipStreamIsCapturing(stream, &capture);
+            if (found > 1 && capture == hipStreamCaptureStatusNone)
+            {
+                hipEvent_t start = nullptr, stop = nullptr;
+                DIT_HIP(hipEventCreate(&start), "hipEventCreate");
+                if (hipEventCreate(&stop) != hipSuccess)
+                {
+                    (void)hipEventDestroy(start);
+                    return fail(AWA_ERR_DEVICE, "hipEventCreate failed");
+                }
+                const float one = 1.f, zero = 0.f;
+                float best = -1.f;
+                for (int i = 0; i < found; i++)
+                {
+                    if (results[i].workspaceSize > kGemmWorkspace)
+                        continue;
+                    auto run = [&]() {
+                        return hipblasLtMatmul(b->lt, g.desc, &one, w, g.a, x, g.b, &zero, y, g.c, y, g.c,
+                                               &results[i].algo, b->lt_workspace, kGemmWorkspace, stream);
+                    };
+                    if (run() != HIPBLAS_STATUS_SUCCESS)
+                        continue;
+                    bool ran = hipEventRecord(start, stream) == hipSuccess;
+                    for (int r = 0; r < kGemmTimedRuns && ran; r++)
+                        ran = run() == HIPBLAS_STATUS_SUCCESS;
+                    float ms = 0.f;
+                    if (!ran || hipEventRecord(stop, stream) != hipSuccess || hipEventSynchronize(stop) != hipSuccess ||
+                        hipEventElapsedTime(&ms, start, stop) != hipSuccess)
+                        continue;
+                    if (best < 0.f || ms < best)
+                    {
+                        best = ms;
+                        g.algo = results[i].algo;
+                    }
+                }
+                (void)hipEventDestroy(start);
+                (void)hipEventDestroy(stop);
+                (void)hipGetLastError();
+            }
+        }
         if (!ok)
         {
             for (hipblasLtMatrixLayout_t l : {g.a, g.b, g.c})
@@ -190,7 +241,6 @@ int gemm(awa_dit_block* b, const void* x, long long ldx, const void* w, void* y,
                 hipblasLtMatmulDescDestroy(g.desc);
             return fail(AWA_ERR_DEVICE, "hipBLASLt has no algorithm for a GEMM of the block");
         }
-        g.algo = result.algo;
         it = b->shapes.emplace(key, g).first;
     }
     const float alpha = 1.f, beta = 0.f;
