@@ -5,7 +5,8 @@
 // query column: the online-softmax statistics of a query live in two lanes
 // (lane and lane^32), and the rescale of the output accumulator O^T = V^T P^T
 // is lane-local. A workgroup is 4 waves (128 query rows; bf16 MFMA) or 8
-// waves (256 query rows; fp32 MFMA), see the variants below.
+// waves (256 query rows; bf16 MFMA single-buffered, or the fp32 MFMA
+// pipeline), see the variants below.
 //
 // K and V tiles (64 keys for bf16, 32 for fp32) are staged through LDS (K
 // row-major, V transposed so that the PV operand reads are contiguous in the
