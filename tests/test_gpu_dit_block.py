@@ -163,3 +163,66 @@ def test_dit_block_benchmark_shape(gpu, precision, shifted):
     print(f"  rel err video {ev:.3g} text {et:.3g}", flush=True)
     tol = 2e-2 if bf16 else 1e-5
     assert ev <= tol and et <= tol
+
+
+def test_dit_stack_zero_gates_is_exact_at_benchmark_shape(gpu):
+    """The whole 32-block loop at the benchmark workload (latent 9x16x16,
+    windows 3x8x8, 64 text, hidden 2560 = 20 x 128, SwiGLU 6912, blocks 0-8
+    fp32 and 9-31 bf16), checked by a property that holds at any size: with
+    every Ada gate zero (the embedding's and the learned ones) each block
+    returns its video and text inputs unchanged, (h + bias) * 0 + x = x
+    exactly, and the last block, with its text output projection and bias
+    zero, returns text as 2 * (0 + text). So video_out = bf16(video) and
+    text_out = 2 * bf16(text) bit for bit, whatever the attention and the
+    MLP compute in between (weights N(0, 0.02) on the device)."""
+    t, h, w, nt, nh, nw, tx = 9, 16, 16, 3, 8, 8, 64
+    blocks, prefix, heads, hidden, mlp = 32, 9, 20, 2560, 6912
+    n = t * h * w
+    print("case dit stack zero gates, 33f 256x256, 32 blocks", flush=True)
+    stack = A.DitStack(t, h, w, nt, nh, nw, tx, blocks, prefix, heads, HEAD_DIM, hidden, mlp, EPS)
+    rng = np.random.default_rng(5)
+    keep = []
+    seed = [700]
+
+    def dev(count, es, stddev=0.02):
+        b = A.DeviceBuffer(count * es)
+        b.fill_normal(count, es, seed[0], None, stddev)
+        seed[0] += 1
+        keep.append(b)
+        return b
+
+    def host(a):
+        a = np.ascontiguousarray(a, np.float32)
+        b = A.DeviceBuffer(a.nbytes)
+        b.upload(a)
+        keep.append(b)
+        return b
+
+    wv, wt = [], []
+    for blk in range(blocks):
+        es = 4 if blk < prefix else 2
+        for br in range(2):
+            ada = (rng.standard_normal((6, hidden)) * 0.5).astype(np.float32)
+            ada[[2, 5]] = 0.0  # learned attention and MLP gates
+            proj = dev(hidden * hidden, es)
+            bias = host(rng.standard_normal(hidden) * 0.1)
+            if br == 1 and blk == blocks - 1:
+                proj.zero()
+                bias.zero()
+            (wv if br == 0 else wt).append(A.AwaDitBranchWeights(
+                dev(3 * hidden * hidden, es).ptr, proj.ptr, bias.ptr, dev(mlp * hidden, es).ptr,
+                dev(mlp * hidden, es).ptr, dev(hidden * mlp, es).ptr,
+                host(rng.uniform(0.5, 1.5, HEAD_DIM)).ptr, host(rng.uniform(0.5, 1.5, HEAD_DIM)).ptr, host(ada).ptr))
+    video = rng.standard_normal((n, hidden)).astype(np.float32)
+    text = rng.standard_normal((tx, hidden)).astype(np.float32)
+    emb = (rng.standard_normal((hidden, 2, 3)) * 0.5).astype(np.float32)
+    emb[:, :, 2] = 0.0  # embedding gates
+    bv, bt, be = host(video), host(text), host(emb)
+    ov, ot = A.DeviceBuffer(n * hidden * 2), A.DeviceBuffer(tx * hidden * 2)
+    stack.run(wv, wt, bv.ptr, bt.ptr, be.ptr, ov.ptr, ot.ptr)
+    A.synchronize()
+    got_v = A.bf16_bits_to_f32(ov.download((n * hidden,), np.uint16)).reshape(n, hidden)
+    got_t = A.bf16_bits_to_f32(ot.download((tx * hidden,), np.uint16)).reshape(tx, hidden)
+    stack.destroy()
+    np.testing.assert_array_equal(got_v, O.round_bf16(video))
+    np.testing.assert_array_equal(got_t, 2.0 * O.round_bf16(text))
