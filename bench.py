@@ -168,9 +168,13 @@ def dit_step(A, stream, steps: int, warmup: int = 2) -> dict:
     for b in range(BLOCKS):
         es = 4 if b < FP32_PREFIX else 2
         for lst in (wv, wt):
+            # proj_in_gate and proj_in in one allocation, back to back (the
+            # block then runs them as one GEMM).
+            mlp_pair = buf(2 * mh * hidden, es)
             lst.append(A.AwaDitBranchWeights(
-                buf(3 * hd * hidden, es), buf(hidden * hd, es), buf(hidden, 4), buf(mh * hidden, es),
-                buf(mh * hidden, es), buf(hidden * mh, es), buf(HEAD_DIM, 4), buf(HEAD_DIM, 4), buf(6 * hidden, 4)))
+                buf(3 * hd * hidden, es), buf(hidden * hd, es), buf(hidden, 4), mlp_pair,
+                mlp_pair + mh * hidden * es, buf(hidden * mh, es), buf(HEAD_DIM, 4), buf(HEAD_DIM, 4),
+                buf(6 * hidden, 4)))
     video, text, emb = buf(N * hidden, 4, 1.0), buf(TEXT * hidden, 4, 1.0), buf(6 * hidden, 4, 1.0)
     vout, tout = buf(N * hidden, 2, 1.0), buf(TEXT * hidden, 2, 1.0)
     stream.synchronize()

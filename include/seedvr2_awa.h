@@ -292,7 +292,8 @@ typedef struct awa_dit_branch_weights {
     const void* proj_out;       /* [hidden][heads*head_dim] */
     const float* proj_out_bias; /* [hidden], 16-byte aligned */
     const void* mlp_gate;       /* [mlp_hidden][hidden] (proj_in_gate) */
-    const void* mlp_in;         /* [mlp_hidden][hidden] (proj_in) */
+    const void* mlp_in;         /* [mlp_hidden][hidden] (proj_in); stored right after mlp_gate, the two
+                                   run as one GEMM of width 2 * mlp_hidden */
     const void* mlp_out;        /* [hidden][mlp_hidden] (proj_out) */
     const float* norm_q;        /* [head_dim], 16-byte aligned */
     const float* norm_k;        /* [head_dim], 16-byte aligned */

@@ -438,10 +438,21 @@ int awa_dit_block_forward(awa_dit_block* b, const awa_dit_branch_weights* video_
         nm.scale = b->ada[br] + 4 * hidden;
         DIT_HIP(awa::launch_rmsnorm_modulate(nm, stream), "rmsnorm_modulate launch");
         char* pair = static_cast<char*>(b->ws[br][kPair]);
-        if ((rc = gemm(b, b->ws[br][kNorm], hidden, W[br]->mlp_gate, pair, 2LL * mh, M, mh, hidden, stream)) !=
-                AWA_OK ||
-            (rc = gemm(b, b->ws[br][kNorm], hidden, W[br]->mlp_in, pair + static_cast<size_t>(mh) * es, 2LL * mh, M,
-                       mh, hidden, stream)) != AWA_OK)
+        // The two input projections fill the halves of one [M][2 mh] buffer.
+        // Weights stored back to back ([mh][hidden] gate, then in) are one
+        // [2 mh][hidden] matrix: one GEMM of twice the width.
+        const bool adjacent = static_cast<const char*>(W[br]->mlp_in) ==
+                              static_cast<const char*>(W[br]->mlp_gate) + static_cast<size_t>(mh) * hidden * es;
+        if (adjacent)
+        {
+            if ((rc = gemm(b, b->ws[br][kNorm], hidden, W[br]->mlp_gate, pair, 2LL * mh, M, 2 * mh, hidden,
+                           stream)) != AWA_OK)
+                return rc;
+        }
+        else if ((rc = gemm(b, b->ws[br][kNorm], hidden, W[br]->mlp_gate, pair, 2LL * mh, M, mh, hidden, stream)) !=
+                     AWA_OK ||
+                 (rc = gemm(b, b->ws[br][kNorm], hidden, W[br]->mlp_in, pair + static_cast<size_t>(mh) * es, 2LL * mh,
+                            M, mh, hidden, stream)) != AWA_OK)
             return rc;
         awa::SwiGlu sg{};
         sg.in = pair;

@@ -23,9 +23,12 @@ pytestmark = pytest.mark.gpu
 
 
 class DeviceBranch:
-    """A branch's weights on the device: GEMM weights in the block's element size."""
+    """A branch's weights on the device: GEMM weights in the block's element
+    size. adjacent_mlp stores proj_in right after proj_in_gate in one
+    allocation (the block then runs the two as one GEMM); otherwise they are
+    separate allocations (two GEMMs)."""
 
-    def __init__(self, w: O.DitBranchWeights, elemsize: int):
+    def __init__(self, w: O.DitBranchWeights, elemsize: int, adjacent_mlp: bool = False):
         self.bufs = []
 
         def up(a, es):
@@ -35,9 +38,14 @@ class DeviceBranch:
             self.bufs.append(buf)
             return buf.ptr
 
+        if adjacent_mlp:
+            gate = up(np.concatenate([w.mlp_gate, w.mlp_in]), elemsize)
+            inp = gate + w.mlp_gate.size * elemsize
+        else:
+            gate, inp = up(w.mlp_gate, elemsize), up(w.mlp_in, elemsize)
         self.struct = A.AwaDitBranchWeights(
-            up(w.qkv, elemsize), up(w.proj_out, elemsize), up(w.proj_out_bias, 4), up(w.mlp_gate, elemsize),
-            up(w.mlp_in, elemsize), up(w.mlp_out, elemsize), up(w.norm_q, 4), up(w.norm_k, 4), up(w.ada, 4))
+            up(w.qkv, elemsize), up(w.proj_out, elemsize), up(w.proj_out_bias, 4), gate, inp,
+            up(w.mlp_out, elemsize), up(w.norm_q, 4), up(w.norm_k, 4), up(w.ada, 4))
 
 
 def upload_act(x, es):
@@ -108,8 +116,8 @@ def test_dit_stack_matches_oracle_blocks(gpu):
     g0, video, text, emb, _, _ = case(300, False)
     ws = [(make_weights(rng), make_weights(rng)) for _ in range(blocks)]
     stack = A.DitStack(*g0.args, g0.text_tokens, blocks, prefix, HEADS, HEAD_DIM, HIDDEN, MLP, EPS)
-    dev = [(DeviceBranch(wv, 4 if b < prefix else 2), DeviceBranch(wt, 4 if b < prefix else 2))
-           for b, (wv, wt) in enumerate(ws)]
+    dev = [(DeviceBranch(wv, 4 if b < prefix else 2, adjacent_mlp=b % 2 == 0),
+            DeviceBranch(wt, 4 if b < prefix else 2, adjacent_mlp=b % 2 == 0)) for b, (wv, wt) in enumerate(ws)]
     bv, bt, be = upload_act(video, 4), upload_act(text, 4), upload_act(emb, 4)
     ov, ot = A.DeviceBuffer(video.size * 2), A.DeviceBuffer(text.size * 2)
     stack.run([d[0].struct for d in dev], [d[1].struct for d in dev], bv.ptr, bt.ptr, be.ptr, ov.ptr, ot.ptr)
@@ -151,7 +159,7 @@ def test_dit_block_benchmark_shape(gpu, precision, shifted):
     video, text, emb = n(g.source_tokens, hidden, sd=1.0), n(g.text_tokens, hidden, sd=1.0), n(hidden * 6, sd=1.0)
     es = 2 if bf16 else 4
     blk = A.DitBlock(*g.args, g.text_tokens, g.shifted, heads, HEAD_DIM, hidden, mlp, False, precision, EPS)
-    dv, dt = DeviceBranch(wv, es), DeviceBranch(wt, es)
+    dv, dt = DeviceBranch(wv, es, adjacent_mlp=True), DeviceBranch(wt, es, adjacent_mlp=True)
     bv, bt, be = upload_act(video, es), upload_act(text, es), upload_act(emb, es)
     ov, ot = A.DeviceBuffer(video.size * es), A.DeviceBuffer(text.size * es)
     blk.forward(dv.struct, dt.struct, bv.ptr, bt.ptr, be.ptr, ov.ptr, ot.ptr)
