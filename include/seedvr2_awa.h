@@ -268,7 +268,11 @@ int awa_stack_block_flops(const awa_stack* stack, double* flops);
  * FP32 prefix blocks); AWA_COMPUTE_BF16: bf16 activations and GEMM weights,
  * fp32 accumulation and arithmetic (the BF16 blocks, dit_stack.cpp:519,
  * :550). The GEMMs are library GEMMs (hipBLASLt). A block or stack object is
- * used by one thread at a time (it caches GEMM descriptors on first use). */
+ * used by one thread at a time (it caches GEMM descriptors on first use). The
+ * first forward of an object times hipBLASLt's candidate algorithms for each
+ * GEMM shape on the caller's operands and stream, waiting for the stream once
+ * per shape (not under graph capture, where the heuristic's first is taken);
+ * later calls are asynchronous. */
 typedef struct awa_dit_block_desc {
     int source_t, source_h, source_w;    /* token grid */
     int windows_t, windows_h, windows_w; /* window counts (params 3/4/5) */
