@@ -22,6 +22,7 @@ import pytest
 
 import oracle as O
 from awa_cases import CONFIGS, RAGGED
+from float64_model import attention64, layer64, rope_apply64, rope_frequencies64
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
@@ -201,9 +202,6 @@ def test_pack_unpack_round_trip(text_order):
 # --------------------------------------------------------------------------
 # RoPE
 
-def rope_frequencies64(axis_dim: int = 42) -> np.ndarray:
-    return 10000.0 ** (-(2.0 * np.arange(axis_dim // 2)) / axis_dim)
-
 
 def window_coordinates(g: O.Geometry) -> np.ndarray:
     """[S][3] RoPE coordinates of every packed row, derived from the windows:
@@ -237,28 +235,6 @@ def test_rope_table_closed_form(name, shifted):
         np.testing.assert_allclose(table[:, 42 * a], np.cos(coords[:, a]), atol=1e-6)
 
 
-def rope_apply64(x: np.ndarray, coords: np.ndarray, mistake: str | None = None) -> np.ndarray:
-    """Interleaved-pair rotation of features 0..125 (dims 126, 127 pass
-    through) with per-axis angles coord * 10000^(-2p/42), in float64."""
-    out = x.astype(np.float64).copy()
-    f = rope_frequencies64()
-    for a in range(3):
-        c = coords[:, a].astype(np.float64)
-        ang = c[:, None] * f[None, :]
-        cs, sn = np.cos(ang), np.sin(ang)
-        if mistake == "sin_sign":
-            sn = -sn
-        e = x[..., 42 * a:42 * a + 42:2].astype(np.float64)
-        o = x[..., 42 * a + 1:42 * a + 42:2].astype(np.float64)
-        shape = (-1,) + (1,) * (x.ndim - 2) + (21,)
-        cs, sn = cs.reshape(shape), sn.reshape(shape)
-        if mistake == "pair_swap":
-            e, o = o, e
-        out[..., 42 * a:42 * a + 42:2] = e * cs - o * sn
-        out[..., 42 * a + 1:42 * a + 42:2] = o * cs + e * sn
-    return out
-
-
 def test_mmrope_forward_matches_closed_form():
     g = geometry("clip_2x16x16", True)
     heads, d = 2, 128
@@ -275,16 +251,6 @@ def test_mmrope_forward_matches_closed_form():
 
 # --------------------------------------------------------------------------
 # Attention
-
-def attention64(q, k, v, scale=None):
-    """softmax(q k^T * scale) v in float64; q, k, v [L][H][d]."""
-    d = q.shape[-1]
-    scale = 1.0 / math.sqrt(d) if scale is None else scale
-    s = np.einsum("qhd,khd->hqk", q.astype(np.float64), k.astype(np.float64)) * scale
-    s -= s.max(-1, keepdims=True)
-    p = np.exp(s)
-    p /= p.sum(-1, keepdims=True)
-    return np.einsum("hqk,khd->qhd", p, v.astype(np.float64))
 
 
 @pytest.mark.parametrize("order", ["cpu", "kahan"])
@@ -311,34 +277,6 @@ def test_attention_orders_agree_and_differ_only_in_rounding():
     a = O.attention(packed, m.cu_seqlens, heads, d, "cpu")
     b = O.attention(packed, m.cu_seqlens, heads, d, "kahan")
     assert np.max(np.abs(a - b)) < 2e-6
-
-
-def layer64(g: O.Geometry, video: np.ndarray, text: np.ndarray, mistake: str | None = None):
-    """The whole AWA layer in float64 from its definition: per window, gather
-    the window's video tokens and the text tokens, rotate Q and K with
-    window-local 3-D RoPE, attend, scatter video rows back and average the
-    text rows over windows."""
-    N = g.source_tokens
-    T = g.text_tokens
-    heads, d = video.shape[2], video.shape[3]
-    vid = np.zeros((N, heads, d))
-    txt = np.zeros((T, heads, d))
-    windows = O.make_windows(g)
-    for t0, t1, h0, h1, w0, w1 in windows:
-        tt, hh, ww = np.meshgrid(np.arange(t0, t1), np.arange(h0, h1), np.arange(w0, w1), indexing="ij")
-        idx = ((tt * g.h + hh) * g.w + ww).reshape(-1)
-        toff = 0 if mistake == "text_offset" else T
-        coords = np.concatenate([
-            np.stack([toff + (tt - t0).reshape(-1), (hh - h0).reshape(-1), (ww - w0).reshape(-1)], 1),
-            np.repeat(np.arange(T)[:, None], 3, 1)])
-        x = np.concatenate([video[idx], text])
-        q = rope_apply64(x[:, 0], coords, mistake)
-        k = rope_apply64(x[:, 1], coords, mistake)
-        scale = 1.0 if mistake == "no_scale" else None
-        o = attention64(q, k, x[:, 2], scale)
-        vid[idx] = o[:len(idx)]
-        txt += o[len(idx):]
-    return vid, txt / len(windows)
 
 
 def test_single_window_layer_is_full_attention_with_3d_rope():
