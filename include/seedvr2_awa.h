@@ -35,12 +35,20 @@ extern "C" {
 #define AWA_ERR_DEVICE (-2)
 #define AWA_ERR_ALLOC (-100)
 
-/* Arithmetic of the attention contractions. AWA_COMPUTE_F32 runs QK^T and PV
- * on fp32 MFMA (the reference's FP32 blocks); AWA_COMPUTE_BF16 rounds Q, K, V
- * and P to bf16 and accumulates in fp32 on bf16 MFMA (BF16 blocks). Softmax
- * statistics are fp32 in both. */
+/* Arithmetic of the attention contractions. AWA_COMPUTE_F32 (the reference's
+ * FP32 blocks) takes fp32 Q, K, V and computes each score q.k nearly exactly
+ * before one fp32 rounding, as the reference's Kahan-sum shaders do: Q and K
+ * rows are split into four signed 7-bit digit slices under a per-row power of
+ * two and multiplied on int8 matrix cores with exact int32 sums; P V uses P as
+ * two bf16 pieces and V as three (the fp32 value) on bf16 matrix cores with
+ * fp32 accumulation. AWA_COMPUTE_BF16 rounds Q, K, V and P to bf16 and
+ * accumulates in fp32 on bf16 MFMA (BF16 blocks). AWA_COMPUTE_F32_MFMA runs
+ * QK^T and PV on fp32 MFMA with plain fp32 accumulation (slower, and less
+ * accurate when scores are large or cancel; kept for comparison). Softmax
+ * statistics are fp32 in all three. */
 #define AWA_COMPUTE_F32 0
 #define AWA_COMPUTE_BF16 1
+#define AWA_COMPUTE_F32_MFMA 2
 
 /* A device blob described the way an ncnn Mat is (elempack 1):
  * dims 1..4 with extents w (fastest), h, d, c; n batches (NCNN_BATCH, 1 when

@@ -23,8 +23,9 @@ AWA_OK = 0
 AWA_ERR_INVALID = -1
 AWA_ERR_DEVICE = -2
 AWA_ERR_ALLOC = -100
-COMPUTE_F32 = 0
+COMPUTE_F32 = 0  # exact-score fp32 kernel (int8 digit slices + bf16 pieces)
 COMPUTE_BF16 = 1
+COMPUTE_F32_MFMA = 2  # fp32 MFMA with plain accumulation (comparison path)
 
 # Every symbol of include/seedvr2_awa.h.
 EXPORTED_SYMBOLS = (

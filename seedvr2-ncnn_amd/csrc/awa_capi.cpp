@@ -167,16 +167,15 @@ int check_plan_uploaded(const awa_plan* plan)
 // their K/V reads.
 constexpr int kXcds = 8;
 
-// Attention kernel variant per arithmetic and geometry. fp32 MFMA takes the
-// 8-wave pipeline (one workgroup per unit of up to 256 rows; its long MFMA
-// tiles hide the softmax and the staging). bf16 MFMA takes the 8-wave
-// single-buffered kernel when its 256-row query blocks leave no more waves
-// idle than 128-row blocks would (each unit's K/V tiles are then staged and
-// rotated once instead of once per 128-row block), else the 4-wave kernel
-// with two workgroups per CU.
-int attention_variant(bool bf16_mfma, const awa_plan& plan)
+// Attention kernel variant per arithmetic and geometry. AWA_COMPUTE_F32_MFMA
+// takes the 8-wave fp32-MFMA pipeline (one workgroup per unit of up to 256
+// rows). The bf16 and the exact-score fp32 kernels take their 8-wave form when
+// its 256-row query blocks leave no more waves idle than 128-row blocks would
+// (each unit's K/V tiles are then staged once instead of once per 128-row
+// block), else the 4-wave form with two workgroups per CU.
+int attention_variant(int compute, const awa_plan& plan)
 {
-    if (!bf16_mfma)
+    if (compute == AWA_COMPUTE_F32_MFMA)
         return awa::kVariantWidePipe;
     long long idle_wide = 0, idle_narrow = 0;
     for (const awa::WindowDesc& w : plan.window_descs)
@@ -187,6 +186,17 @@ int attention_variant(bool bf16_mfma, const awa_plan& plan)
         idle_narrow += (L + awa::kQueryRows - 1) / awa::kQueryRows * (awa::kQueryRows / 32) - waves;
     }
     return idle_wide <= idle_narrow ? awa::kVariantWide : awa::kVariantNarrow;
+}
+
+bool valid_compute(int compute)
+{
+    return compute == AWA_COMPUTE_F32 || compute == AWA_COMPUTE_BF16 || compute == AWA_COMPUTE_F32_MFMA;
+}
+
+// The attention kernel for the compute mode.
+hipError_t launch_attention_for(int compute, const awa::AttentionLaunch& p, hipStream_t stream)
+{
+    return compute == AWA_COMPUTE_F32 ? awa::launch_attention_x(p, stream) : awa::launch_attention(p, stream);
 }
 
 // Query rows of a (window, head) unit of L rows as work items of at most
@@ -661,7 +671,7 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
         return rc;
     if (!video_qkv || !text_qkv || !video_out || !text_out)
         return fail(AWA_ERR_INVALID, "null blob");
-    if (compute != AWA_COMPUTE_F32 && compute != AWA_COMPUTE_BF16)
+    if (!valid_compute(compute))
         return fail(AWA_ERR_INVALID, "unknown compute mode");
     trace_blob("forward.video.in", video_qkv);
     trace_blob("forward.text.in", text_qkv);
@@ -728,7 +738,7 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
         p.norm_eps = norm->eps;
     }
     p.windows = plan->dev.windows;
-    p.variant = attention_variant(p.bf16_mfma, *plan);
+    p.variant = attention_variant(compute, *plan);
     p.work = p.variant != awa::kVariantNarrow ? plan->work_wide : plan->work;
     p.work_count = p.variant != awa::kVariantNarrow ? plan->work_wide_count : plan->work_count;
     p.rope_cs = plan->dev.rope_cs;
@@ -739,7 +749,7 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
     p.source_h = plan->source_h;
     p.source_w = plan->source_w;
     p.scale_log2 = (1.f / std::sqrt(static_cast<float>(vl.head_dim))) * 1.4426950408889634f;
-    HIP_TRY(awa::launch_attention(p, stream), "attention kernel launch");
+    HIP_TRY(launch_attention_for(compute, p, stream), "attention kernel launch");
     if (after_attention)
         HIP_TRY(hipEventRecord(after_attention, stream), "hipEventRecord");
     HIP_TRY(awa::launch_text_mean(plan->text_partials, p.text_partial_elemsize, static_cast<int>(plan->windows.size()),
@@ -826,7 +836,7 @@ int awa_window_attention(const awa_plan* plan, const awa_blob* input, const awa_
         return rc;
     if (!input || !output)
         return fail(AWA_ERR_INVALID, "null blob");
-    if (compute != AWA_COMPUTE_F32 && compute != AWA_COMPUTE_BF16)
+    if (!valid_compute(compute))
         return fail(AWA_ERR_INVALID, "unknown compute mode");
     trace_blob("attention.in", input);
     if (!input->data || input->dims != 3 || input->w <= 0 || input->h <= 0 || input->h % 3 != 0 ||
@@ -863,7 +873,7 @@ int awa_window_attention(const awa_plan* plan, const awa_blob* input, const awa_
     p.packed_out_row = output->cstep;
     p.windows = plan->dev.windows;
     // Same variant choice as the fused layer, so that both give the same bits.
-    p.variant = attention_variant(p.bf16_mfma, *plan);
+    p.variant = attention_variant(compute, *plan);
     p.work = p.variant != awa::kVariantNarrow ? plan->work_wide : plan->work;
     p.work_count = p.variant != awa::kVariantNarrow ? plan->work_wide_count : plan->work_count;
     p.max_window_tokens = plan->max_window_tokens;
@@ -872,7 +882,7 @@ int awa_window_attention(const awa_plan* plan, const awa_blob* input, const awa_
     p.source_h = plan->source_h;
     p.source_w = plan->source_w;
     p.scale_log2 = (1.f / std::sqrt(static_cast<float>(head_dim))) * 1.4426950408889634f;
-    HIP_TRY(awa::launch_attention(p, s), "attention kernel launch");
+    HIP_TRY(launch_attention_for(compute, p, s), "attention kernel launch");
     return AWA_OK;
 }
 

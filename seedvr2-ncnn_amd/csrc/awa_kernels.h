@@ -74,6 +74,15 @@ struct AttentionLaunch
 
 hipError_t launch_attention(const AttentionLaunch& p, hipStream_t stream);
 
+// fp32 window attention with nearly exact scores: Q/K as int8 digit slices
+// on int8 MFMA (exact int32 sums), P V as bf16 pieces on bf16 MFMA
+// (AWA_COMPUTE_F32). Variants kVariantNarrow / kVariantWide.
+hipError_t launch_attention_x(const AttentionLaunch& p, hipStream_t stream);
+// LDS of one workgroup of that kernel: static tiles (double-buffered in the
+// 8-wave form), and the dynamic RoPE / row tables for a launch.
+size_t attention_x_static_lds(bool wide);
+size_t attention_x_dynamic_lds(const AttentionLaunch& p, bool norm);
+
 // text_out[k][head][:] = (sum_w partials[w][k][head][:]) / nwin, window order.
 hipError_t launch_text_mean(const void* partials, int partial_elemsize, int window_count, int text_tokens, int heads, int head_dim,
                             void* text_out, long long text_token_stride, int out_elemsize, hipStream_t stream);

@@ -1,0 +1,129 @@
+"""fp32 parity at real-model Q/K magnitudes.
+
+The reference moved its fp32 score and value shaders to Kahan sums because
+fp32 validation must handle cancellation in real-model Q/K
+(src/awa/shader/awa_attention_score.comp:25-47). These tests feed the fused
+fp32 layer Q/K that make the scores large or cancelling:
+
+- Q and K scaled by 8 or 16;
+- Q and K sharing a large common direction per head, so every score carries
+  a large constant that the softmax cancels;
+- the DiT q/k RMSNorm fused into the gather, with gammas up to 10 or 20, on
+  raw projections (x3), with and without a shared direction.
+
+Each case is compared with the Kahan-order oracle (the reference's GPU
+arithmetic), the CPU-order oracle (its CPU layers' plain sums) and the
+float64 definition of the layer. A score of magnitude |s| carries an
+unavoidable fp32 rounding of about 2^-24 |s|, so at the largest magnitudes
+the oracle itself is more than the fp32 budget (1e-4) away from float64, and
+so is an exactly rounded fp32 computation. The gate is therefore:
+
+- max abs error against the oracle <= 1e-4 wherever the oracle is itself
+  within 4e-5 of float64 (two fifths of the budget);
+- everywhere, max abs error against float64 <= max(1e-4, 2 x the oracle's
+  own error against float64): as close to the exact result as the
+  reference's GPU arithmetic, up to the spread of a maximum over rounding
+  errors (exactly rounded scores reach 1.65 x);
+- everywhere, no further from float64 than the reference's CPU arithmetic
+  where that is beyond the budget.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import awa_hip as A
+import oracle as O
+from awa_cases import CONFIGS, HEAD_DIM, abs_err, geometry, qkv_inputs
+from device_blobs import mat3, qkv_blob, read_mat3, read_video, video_out_blob
+from float64_model import layer64
+
+pytestmark = pytest.mark.gpu
+
+FP32_ATOL = 1e-4
+ORACLE_ACCURATE = 4e-5
+EPS = 1e-5
+HEADS = 4
+
+SCENARIOS = ["qk_x4", "qk_x8", "qk_x16", "mean_x2", "mean_x4", "mean_x8", "norm_g5", "norm_g10", "norm_g20",
+             "norm_g10_mean", "norm_g20_mean"]
+
+
+def scenario_inputs(g, name: str, seed: int):
+    """Raw QKV [T][3][H][d] for the scenario, plus the four q/k RMSNorm gammas
+    (None when the scenario feeds the layer directly)."""
+    video, text = qkv_inputs(g, HEADS, HEAD_DIM, seed)
+    rng = np.random.RandomState(seed % 2**31)
+    gammas = None
+    if name.startswith("qk_x"):
+        s = float(name[4:])
+        video[:, :2] *= s
+        text[:, :2] *= s
+    elif name.startswith("mean_x"):
+        s = float(name[6:])
+        m = (s * rng.randn(HEADS, HEAD_DIM)).astype(np.float32)
+        video[:, :2] += m
+        text[:, :2] += m
+    else:
+        gmax = float(name.split("_")[1][1:])
+        video[:, :2] *= 3.0
+        text[:, :2] *= 3.0
+        video[:, 2] *= 3.0
+        text[:, 2] *= 3.0
+        if name.endswith("_mean"):
+            m = (3.0 * rng.randn(HEADS, HEAD_DIM)).astype(np.float32)
+            video[:, :2] += m
+            text[:, :2] += m
+        gammas = [rng.uniform(0.0, gmax, HEAD_DIM).astype(np.float32) for _ in range(4)]
+    return video.astype(np.float32), text.astype(np.float32), gammas
+
+
+def run_layer(g, video, text, gammas):
+    plan = A.Plan(A.LayerParams(*g.args, g.text_tokens, g.shifted))
+    plan.upload()
+    vq, tq = qkv_blob(video, "a", 4), qkv_blob(text, "a", 4)
+    vo = video_out_blob(g.t, g.h, g.w, HEADS, HEAD_DIM, 4, False)
+    to = mat3(HEAD_DIM, HEADS, g.text_tokens, 4)
+    keep = None
+    if gammas is None:
+        plan.forward(vq.blob, tq.blob, vo.blob, to.blob, A.COMPUTE_F32)
+    else:
+        keep = [A.DeviceBuffer(HEAD_DIM * 4) for _ in gammas]
+        for b, x in zip(keep, gammas):
+            b.upload(x)
+        norm = A.AwaQkNorm(*[b.ptr for b in keep], EPS)
+        plan.forward_qknorm(vq.blob, tq.blob, norm, vo.blob, to.blob, A.COMPUTE_F32)
+    A.synchronize()
+    return read_video(vo, g.t, g.h, g.w, HEADS, HEAD_DIM), read_mat3(to)
+
+
+@pytest.mark.parametrize("name,shifted", [("image_1x16x16", False), ("clip_9x16x16", False), ("clip_9x16x16", True)])
+def test_fp32_large_magnitudes(gpu, name, shifted):
+    g = geometry(CONFIGS[name], shifted)
+    failures = []
+    for i, scen in enumerate(SCENARIOS):
+        print(f"case {name} shifted={shifted} {scen}", flush=True)
+        raw_v, raw_t, gammas = scenario_inputs(g, scen, 20260830 + 17 * i)
+        got_v, got_t = run_layer(g, raw_v, raw_t, gammas)
+        video, text = (raw_v, raw_t) if gammas is None else O.qk_norm_inputs(raw_v, raw_t, gammas, EPS)
+        ref_v, ref_t = O.awa_layer(g, video, text, HEADS, HEAD_DIM)
+        cpu_v, cpu_t = O.awa_layer(g, video, text, HEADS, HEAD_DIM, attention_order="cpu", text_order="cpu")
+        ex_v, ex_t = layer64(g, video, text)
+        got = np.concatenate([got_v.ravel(), got_t.ravel()])
+        ref = np.concatenate([ref_v.ravel(), ref_t.ravel()])
+        cpu = np.concatenate([cpu_v.ravel(), cpu_t.ravel()])
+        ex = np.concatenate([ex_v.ravel(), ex_t.ravel()])
+        e_oracle = abs_err(got, ref)
+        e_exact = abs_err(got, ex)
+        oracle_exact = abs_err(ref, ex)
+        cpu_exact = abs_err(cpu, ex)
+        print(f"  {scen:14s} vs oracle {e_oracle:.2e}  vs float64 {e_exact:.2e}  oracle vs float64 {oracle_exact:.2e}"
+              f"  cpu-order oracle vs float64 {cpu_exact:.2e}", flush=True)
+        if oracle_exact <= ORACLE_ACCURATE and e_oracle > FP32_ATOL:
+            failures.append((scen, "oracle", e_oracle))
+        if e_exact > max(FP32_ATOL, 2.0 * oracle_exact):
+            failures.append((scen, "float64", e_exact, oracle_exact))
+        if e_exact > max(FP32_ATOL, cpu_exact):
+            failures.append((scen, "cpu-order", e_exact, cpu_exact))
+    assert not failures, failures
