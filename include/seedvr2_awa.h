@@ -66,7 +66,8 @@ typedef struct awa_blob {
 /* Layer parameters, with the reference's param ids (src/awa/awa_layers.cpp:90-114, :872):
  * 0/1/2 source_t/h/w (-1,-1,-1 = take them from the runtime spec, as the
  * dynamic model package does), 3/4/5 window COUNTS along t/h/w over the grid
- * rescaled to area 45x80, 6 text tokens, 7 shifted, 8 rope_dim (0 = default 126).
+ * rescaled to area 45x80, 6 text tokens, 7 shifted, 8 rope_dim (a positive
+ * multiple of 6; the reference's layer defaults an absent param 8 to 126).
  * runtime_* is the AwaRuntimeSpec (src/awa/awa_layers.h:31-39); set
  * runtime_tokens = 0 when there is none. */
 typedef struct awa_plan_desc {

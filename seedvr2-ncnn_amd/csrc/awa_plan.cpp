@@ -76,7 +76,8 @@ int build_plan(const awa_plan_desc& desc, awa_plan& plan, std::string& error)
         error = "invalid layer params: grid, window counts and text tokens must be positive";
         return AWA_ERR_INVALID;
     }
-    const int rope_dim = desc.rope_dim == 0 ? 126 : desc.rope_dim;
+    // src/awa/awa_layers.cpp:872-874: rope_dim must be positive and a multiple of 6.
+    const int rope_dim = desc.rope_dim;
     if (rope_dim <= 0 || rope_dim % 6 != 0)
     {
         error = "rope_dim must be a positive multiple of 6";

@@ -35,6 +35,7 @@ std::vector<AwaWindow> make_awa_windows(int source_t, int source_h, int source_w
     desc.windows_w = windows_w;
     desc.text_tokens = 1; // the partition does not depend on the text length
     desc.shifted = shifted ? 1 : 0;
+    desc.rope_dim = 126;
     if (source_t <= 0 || source_h <= 0 || source_w <= 0)
         return {};
     awa_plan* plan = nullptr;

@@ -95,8 +95,14 @@ int run_params()
     ParamDict pd = params(2, 16, 16, 1, 8, 8, 64, 1);
     pd.set(8, 125);
     expect(rope->load_param(pd) == -1, "rope_dim must be a multiple of 6");
+    pd.set(8, 0);
+    expect(rope->load_param(pd) == -1, "rope_dim 0 is invalid (only an absent param 8 defaults to 126)");
+    pd.set(8, -6);
+    expect(rope->load_param(pd) == -1, "negative rope_dim is invalid");
     pd.set(8, 126);
     expect(rope->load_param(pd) == 0, "rope_dim 126");
+    ParamDict absent = params(2, 16, 16, 1, 8, 8, 64, 1);
+    expect(rope->load_param(absent) == 0, "absent param 8 defaults to 126");
     const auto windows = seedvr2::make_awa_windows(2, 16, 16, 1, 8, 8, true);
     expect(windows.size() == 9 && windows[1].h0 == 4 && windows[1].h1 == 12 && windows[3].w0 == 4,
            "make_awa_windows 2x16x16 shifted");

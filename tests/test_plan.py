@@ -80,6 +80,7 @@ def test_runtime_spec_dynamic_params():
     ((1, 16, 16, 1, 8, 8, 0, False, 126), None),
     ((1, 16, 16, 1, 8, 8, 64, False, 100), None),   # rope_dim not a multiple of 6
     ((1, 16, 16, 1, 8, 8, 64, False, -6), None),
+    ((1, 16, 16, 1, 8, 8, 64, False, 0), None),     # rope_dim 0 (src/awa/awa_layers.cpp:873-874)
     ((-1, -1, -1, 1, 8, 8, 64, False, 126), None),  # dynamic without runtime spec
     ((-1, -1, -1, 1, 8, 8, 64, False, 126), (2, 16, 16, 500)),  # inconsistent spec
     ((-1, 16, 16, 1, 8, 8, 64, False, 126), None),  # partial -1
