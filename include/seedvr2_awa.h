@@ -69,7 +69,10 @@ typedef struct awa_blob {
  * rescaled to area 45x80, 6 text tokens, 7 shifted, 8 rope_dim (a positive
  * multiple of 6; the reference's layer defaults an absent param 8 to 126).
  * runtime_* is the AwaRuntimeSpec (src/awa/awa_layers.h:31-39); set
- * runtime_tokens = 0 when there is none. */
+ * runtime_tokens = 0 when there is none. heads (no reference counterpart:
+ * the layers learn it from the input blob) is optional: when positive,
+ * awa_plan_upload also builds the attention work list for that head count,
+ * which awa_forward_noalloc needs; 0 leaves it to the first forward. */
 typedef struct awa_plan_desc {
     int source_t, source_h, source_w;
     int windows_t, windows_h, windows_w;
@@ -77,6 +80,7 @@ typedef struct awa_plan_desc {
     int shifted;
     int rope_dim;
     int runtime_t, runtime_h, runtime_w, runtime_tokens;
+    int heads;
 } awa_plan_desc;
 
 typedef struct awa_plan_info {
@@ -163,6 +167,23 @@ int awa_qkv_shape(const awa_blob* qkv, int tokens, int* heads, int* head_dim);
  * Requires head_dim 128 and rope_dim 126; other shapes use the staged entry points. */
 int awa_forward(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv, const awa_blob* video_out,
                 const awa_blob* text_out, int compute, void* stream);
+
+/* awa_forward that allocates no device memory. No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The
+ * per-window text rows, which awa_forward keeps in a workspace the plan
+ * allocates on first use, go to a static device buffer of
+ * AWA_NOALLOC_SCRATCH_BYTES per GPU instead. Limits: nwin * T_x * H * d *
+ * text_out.elemsize must not exceed the buffer (else AWA_ERR_INVALID), and the
+ * plan must already hold the work list for the blobs' head count (built by
+ * awa_plan_upload when awa_plan_desc.heads names it, or by an earlier
+ * awa_forward with that head count; else AWA_ERR_INVALID). Every call on a
+ * GPU uses that GPU's one buffer, which keeps the last call's contents:
+ * calls that overlap on one GPU (other streams or threads) race. Same blobs,
+ * compute modes and results as awa_forward. */
+#define AWA_NOALLOC_SCRATCH_BYTES (32u << 20)
+int awa_forward_noalloc(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv,
+                        const awa_blob* video_out, const awa_blob* text_out, int compute, void* stream);
 
 /* The DiT block's q/k RMSNorm (affine, fp32 arithmetic and output): for every
  * token and head, x * (1 / sqrt(mean(x^2 over head_dim) + eps)) * gamma, with

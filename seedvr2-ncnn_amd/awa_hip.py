@@ -35,7 +35,7 @@ EXPORTED_SYMBOLS = (
     "awa_event_synchronize", "awa_event_elapsed_ms", "awa_fill_normal", "awa_fill_normal_scaled", "awa_plan_create", "awa_plan_destroy",
     "awa_plan_info_get", "awa_plan_windows", "awa_plan_sequence_index", "awa_plan_cu_seqlens",
     "awa_plan_video_positions", "awa_plan_text_positions", "awa_plan_rope_table", "awa_plan_upload",
-    "awa_qkv_shape", "awa_forward", "awa_forward_qknorm", "awa_rmsnorm", "awa_qkv_concat", "awa_pack", "awa_mmrope",
+    "awa_qkv_shape", "awa_forward", "awa_forward_noalloc", "awa_forward_qknorm", "awa_rmsnorm", "awa_qkv_concat", "awa_pack", "awa_mmrope",
     "awa_window_attention", "awa_unpack", "awa_cast",
     "awa_stack_create", "awa_stack_destroy", "awa_stack_run", "awa_stack_set_profiling", "awa_stack_set_graph", "awa_stack_block_times",
     "awa_stack_block_flops", "awa_dit_block_create", "awa_dit_block_destroy", "awa_dit_block_forward",
@@ -73,7 +73,7 @@ class AwaBlob(ctypes.Structure):
 class AwaPlanDesc(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int) for name in (
         "source_t", "source_h", "source_w", "windows_t", "windows_h", "windows_w", "text_tokens", "shifted",
-        "rope_dim", "runtime_t", "runtime_h", "runtime_w", "runtime_tokens")]
+        "rope_dim", "runtime_t", "runtime_h", "runtime_w", "runtime_tokens", "heads")]
 
 
 class AwaStackDesc(ctypes.Structure):
@@ -149,6 +149,7 @@ def lib() -> ctypes.CDLL:
         L.awa_plan_upload.argtypes = [vp, vp]
         bp = ctypes.POINTER(AwaBlob)
         L.awa_forward.argtypes = [vp, bp, bp, bp, bp, i, vp]
+        L.awa_forward_noalloc.argtypes = [vp, bp, bp, bp, bp, i, vp]
         L.awa_forward_qknorm.argtypes = [vp, bp, bp, ctypes.POINTER(AwaQkNorm), bp, bp, i, vp]
         L.awa_rmsnorm.argtypes = [bp, vp, ctypes.c_float, bp, vp]
         L.awa_qkv_concat.argtypes = [bp, bp, bp, bp, vp]
@@ -330,9 +331,11 @@ class LayerParams:
 
 
 class Plan:
-    def __init__(self, params: LayerParams, runtime: Optional[Sequence[int]] = None):
+    def __init__(self, params: LayerParams, runtime: Optional[Sequence[int]] = None, heads: int = 0):
+        """heads > 0: awa_plan_upload also builds the work list for that head
+        count (what forward_noalloc needs)."""
         desc = AwaPlanDesc(params.t, params.h, params.w, params.nt, params.nh, params.nw, params.text_tokens,
-                           int(params.shifted), params.rope_dim, 0, 0, 0, 0)
+                           int(params.shifted), params.rope_dim, 0, 0, 0, 0, heads)
         if runtime is not None:
             desc.runtime_t, desc.runtime_h, desc.runtime_w, desc.runtime_tokens = runtime
         p = ctypes.c_void_p()
@@ -389,6 +392,12 @@ class Plan:
                 compute: int, stream: Optional[Stream] = None) -> None:
         check(lib().awa_forward(self.h, ctypes.byref(video_qkv), ctypes.byref(text_qkv), ctypes.byref(video_out),
                                 ctypes.byref(text_out), compute, _s(stream)), "awa_forward")
+
+    def forward_noalloc(self, video_qkv: AwaBlob, text_qkv: AwaBlob, video_out: AwaBlob, text_out: AwaBlob,
+                        compute: int, stream: Optional[Stream] = None) -> int:
+        """awa_forward_noalloc; returns its code (callers check rejections)."""
+        return lib().awa_forward_noalloc(self.h, ctypes.byref(video_qkv), ctypes.byref(text_qkv),
+                                         ctypes.byref(video_out), ctypes.byref(text_out), compute, _s(stream))
 
     def forward_qknorm(self, video_qkv: AwaBlob, text_qkv: AwaBlob, norm: AwaQkNorm, video_out: AwaBlob,
                        text_out: AwaBlob, compute: int = COMPUTE_F32, stream: Optional[Stream] = None) -> None:

@@ -610,7 +610,7 @@ int awa_plan_rope_table(const awa_plan* plan, float* out)
     return AWA_OK;
 }
 
-int awa_plan_upload(awa_plan* plan, void* stream)
+static int awa_plan_upload_tables(awa_plan* plan, void* stream)
 {
     if (!plan)
         return fail(AWA_ERR_INVALID, "null plan");
@@ -631,6 +631,30 @@ int awa_plan_upload(awa_plan* plan, void* stream)
     HIP_TRY(hipStreamSynchronize(s), "plan upload sync");
     plan->dev.device = device;
     return AWA_OK;
+}
+
+} // extern "C"
+
+namespace
+{
+
+// The plan's device tables, then its attention work list when the plan
+// desc named the head count.
+int upload_plan(awa_plan* plan, void* stream)
+{
+    const int rc = awa_plan_upload_tables(plan, stream);
+    if (rc != AWA_OK || plan->heads_hint <= 0)
+        return rc;
+    return ensure_workspace(*plan, plan->heads_hint, 0);
+}
+
+} // namespace
+
+extern "C" {
+
+int awa_plan_upload(awa_plan* plan, void* stream)
+{
+    return upload_plan(plan, stream);
 }
 
 // ---- forward ----
@@ -664,7 +688,7 @@ void set_error(const std::string& message)
 
 int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv, const awa_qk_norm* norm,
                   const awa_blob* video_out, const awa_blob* text_out, int compute, hipStream_t stream,
-                  hipEvent_t after_attention)
+                  hipEvent_t after_attention, const Scratch* scratch)
 {
     int rc = check_plan_uploaded(plan);
     if (rc != AWA_OK)
@@ -715,10 +739,31 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
             return fail(AWA_ERR_INVALID, "norm eps must be finite and non-negative");
     }
 
-    const size_t partial_bytes = plan->windows.size() * static_cast<size_t>(plan->text_tokens) * vl.heads *
-                                 vl.head_dim * sizeof(float);
-    if ((rc = ensure_workspace(*plan, vl.heads, partial_bytes)) != AWA_OK)
-        return rc;
+    void* partials = nullptr;
+    if (scratch)
+    {
+        // No allocation: the text rows in the caller's buffer, the work list
+        // already on the device.
+        const size_t need = plan->windows.size() * static_cast<size_t>(plan->text_tokens) * vl.heads *
+                            vl.head_dim * static_cast<size_t>(text_out->elemsize);
+        if (need > scratch->bytes)
+            return fail(AWA_ERR_INVALID, "text rows of this layer need " + std::to_string(need) +
+                                             " bytes, more than the no-alloc scratch buffer's " +
+                                             std::to_string(scratch->bytes));
+        std::lock_guard<std::mutex> lock(plan->mutex);
+        if (plan->work_heads != vl.heads || !plan->work)
+            return fail(AWA_ERR_INVALID, "plan has no work list for " + std::to_string(vl.heads) +
+                                             " heads: create it with awa_plan_desc.heads set, or run awa_forward once");
+        partials = scratch->ptr;
+    }
+    else
+    {
+        const size_t partial_bytes = plan->windows.size() * static_cast<size_t>(plan->text_tokens) * vl.heads *
+                                     vl.head_dim * sizeof(float);
+        if ((rc = ensure_workspace(*plan, vl.heads, partial_bytes)) != AWA_OK)
+            return rc;
+        partials = plan->text_partials;
+    }
 
     awa::AttentionLaunch p{};
     p.fused = true;
@@ -726,7 +771,7 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
     p.video = {video_qkv->data, vl.token_stride, vl.qkv_stride, elem};
     p.text = {text_qkv->data, tl.token_stride, tl.qkv_stride, elem};
     p.video_out = sink;
-    p.text_partials = plan->text_partials;
+    p.text_partials = partials;
     p.text_partial_elemsize = static_cast<int>(text_out->elemsize);
     if (norm)
     {
@@ -752,7 +797,7 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
     HIP_TRY(launch_attention_for(compute, p, stream), "attention kernel launch");
     if (after_attention)
         HIP_TRY(hipEventRecord(after_attention, stream), "hipEventRecord");
-    HIP_TRY(awa::launch_text_mean(plan->text_partials, p.text_partial_elemsize, static_cast<int>(plan->windows.size()),
+    HIP_TRY(awa::launch_text_mean(partials, p.text_partial_elemsize, static_cast<int>(plan->windows.size()),
                                   plan->text_tokens,
                                   vl.heads, vl.head_dim, text_out->data, text_out->cstep, text_out->elemsize, stream),
             "text mean kernel launch");

@@ -14,11 +14,21 @@ namespace awa
 // Sets the calling thread's awa_last_error() text.
 void set_error(const std::string& message);
 
+// Caller-provided device memory for the per-window text rows.
+struct Scratch
+{
+    void* ptr;
+    size_t bytes;
+};
+
 // awa_forward (norm null) or awa_forward_qknorm, with an optional event
 // recorded between the attention kernel and the text-mean kernel (for
-// per-kernel timing).
+// per-kernel timing). scratch null: the text rows go to the plan's
+// workspace (allocated on first use, with the work list). scratch set: they
+// go there, and nothing is allocated; the plan must already hold the work
+// list for the head count.
 int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv, const awa_qk_norm* norm,
                   const awa_blob* video_out, const awa_blob* text_out, int compute, hipStream_t stream,
-                  hipEvent_t after_attention);
+                  hipEvent_t after_attention, const Scratch* scratch = nullptr);
 
 } // namespace awa

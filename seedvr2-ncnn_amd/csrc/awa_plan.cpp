@@ -83,6 +83,12 @@ int build_plan(const awa_plan_desc& desc, awa_plan& plan, std::string& error)
         error = "rope_dim must be a positive multiple of 6";
         return AWA_ERR_INVALID;
     }
+    if (desc.heads < 0)
+    {
+        error = "heads must be 0 (unknown) or positive";
+        return AWA_ERR_INVALID;
+    }
+    plan.heads_hint = desc.heads;
 
     plan.source_t = st;
     plan.source_h = sh;

@@ -71,6 +71,7 @@ struct awa_plan
     int text_tokens = 0;
     bool shifted = false;
     int rope_dim = 126;
+    int heads_hint = 0; // awa_plan_desc.heads: work list built at upload when positive
     int window_t = 0, window_h = 0, window_w = 0;
 
     std::vector<awa::Box> windows;

@@ -105,6 +105,7 @@ int awa_stack_create(const awa_stack_desc* desc, awa_stack** stack)
         pd.text_tokens = desc->text_tokens;
         pd.shifted = shifted;
         pd.rope_dim = 126;
+        pd.heads = desc->heads;
         int rc = awa_plan_create(&pd, &s->plans[shifted]);
         if (rc == AWA_OK)
             rc = awa_plan_upload(s->plans[shifted], nullptr);

@@ -297,6 +297,7 @@ int awa_dit_block_create(const awa_dit_block_desc* desc, awa_dit_block** out)
     pd.text_tokens = desc->text_tokens;
     pd.shifted = desc->shifted;
     pd.rope_dim = 126;
+    pd.heads = desc->heads;
     int rc = awa_plan_create(&pd, &b->plan);
     if (rc != AWA_OK || (rc = awa_plan_upload(b->plan, nullptr)) != AWA_OK)
     {

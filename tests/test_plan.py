@@ -92,6 +92,13 @@ def test_plan_rejects_invalid_params(params, runtime):
     assert e.value.code == A.AWA_ERR_INVALID
 
 
+def test_plan_rejects_negative_heads():
+    """awa_plan_desc.heads: 0 (unknown) or a positive head count."""
+    with pytest.raises(A.AwaError) as e:
+        A.Plan(A.LayerParams(1, 16, 16, 1, 8, 8, 64), heads=-1)
+    assert e.value.code == A.AWA_ERR_INVALID
+
+
 def test_forward_requires_uploaded_plan():
     """Entry points refuse a plan that was never uploaded (the reference's
     'uninitialized Vulkan state', awa_layers.cpp:506-510), before touching memory."""
