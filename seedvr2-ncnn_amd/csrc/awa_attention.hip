@@ -817,13 +817,27 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
 
 } // namespace
 
+size_t attention_static_lds(bool bf16_mfma, int variant)
+{
+    // K tile (keys x padded head_dim) and transposed V tile (head_dim x padded
+    // keys): 64 bf16 keys or 32 fp32 keys; double-buffered in the pipeline.
+    const size_t tiles = bf16_mfma ? 64 * (kHeadDim + 8) * 2 + kHeadDim * (64 + 8) * 2
+                                   : 32 * (kHeadDim + 4) * 4 + kHeadDim * (32 + 4) * 4;
+    return (variant == kVariantWidePipe ? 2 : 1) * tiles;
+}
+
+size_t attention_dynamic_lds(const AttentionLaunch& p)
+{
+    // Norm gammas, RoPE table, then the row table: K and V row offsets and one
+    // coordinate word per row, padded to whole 64-row tiles.
+    const size_t row_table = static_cast<size_t>((p.max_window_tokens + 63) & ~63) * (2 * sizeof(long long) + 4);
+    return (p.qk_norm ? 2 * kHeadDim * 4 : 0) + rope_table_bytes(p.fused, p.rope_coords) + row_table;
+}
+
 template <typename TIn, typename TOut, bool BF16, bool FUSED, int VARIANT, bool NORM>
 static hipError_t launch_one(const AttentionLaunch& p, hipStream_t stream)
 {
-    // RoPE table, then the row table: K and V row offsets and one coordinate
-    // word per row, padded to whole 64-row tiles.
-    const size_t row_table = static_cast<size_t>((p.max_window_tokens + 63) & ~63) * (2 * sizeof(long long) + 4);
-    const size_t dynamic_lds = kNormLdsBytes<NORM> + rope_table_bytes(FUSED, p.rope_coords) + row_table;
+    const size_t dynamic_lds = attention_dynamic_lds(p);
     hipLaunchKernelGGL((window_attention_kernel<TIn, TOut, BF16, FUSED, VARIANT, NORM>), dim3(p.work_count),
                        dim3(VARIANT != kVariantNarrow ? 512 : 256), dynamic_lds, stream, p);
     return hipGetLastError();

@@ -188,6 +188,42 @@ int attention_variant(int compute, const awa_plan& plan)
     return idle_wide <= idle_narrow ? awa::kVariantWide : awa::kVariantNarrow;
 }
 
+// The variant to launch: attention_variant's choice, or, for the
+// exact-score fp32 kernel, its single-buffered 4-wave form when the
+// double-buffered 8-wave form's tiles and tables exceed a workgroup's LDS.
+// Returns -1 with the reason set when no variant fits the window.
+int launch_variant(int compute, const awa_plan& plan, awa::AttentionLaunch& p)
+{
+    if (plan.max_window_tokens >= awa::kMaxWindowRows)
+        return fail(AWA_ERR_INVALID, "window of " + std::to_string(plan.max_window_tokens) +
+                                         " rows exceeds the attention kernels' " +
+                                         std::to_string(awa::kMaxWindowRows - 1) + "-row limit");
+    p.variant = attention_variant(compute, plan);
+    auto lds = [&](int variant, const awa::AttentionLaunch& q) {
+        if (compute == AWA_COMPUTE_F32)
+            return awa::attention_x_static_lds(variant == awa::kVariantWide) +
+                   awa::attention_x_dynamic_lds(q, q.qk_norm);
+        return awa::attention_static_lds(compute == AWA_COMPUTE_BF16, variant) + awa::attention_dynamic_lds(q);
+    };
+    // The 8-wave fallback is decided on the fused layer's tables (RoPE table
+    // and norm gammas included), so that the staged and fused layers of one
+    // plan take the same variant and give the same bits.
+    awa::AttentionLaunch fused = p;
+    fused.fused = true;
+    fused.qk_norm = true;
+    fused.rope_coords = plan.rope_coords;
+    if (compute == AWA_COMPUTE_F32 && p.variant == awa::kVariantWide && lds(p.variant, fused) > awa::kWorkgroupLds)
+        p.variant = awa::kVariantNarrow;
+    if (lds(p.variant, p) > awa::kWorkgroupLds)
+        return fail(AWA_ERR_INVALID, "window of " + std::to_string(plan.max_window_tokens) +
+                                         " rows needs " + std::to_string(lds(p.variant, p)) +
+                                         " bytes of LDS per workgroup, more than " +
+                                         std::to_string(awa::kWorkgroupLds));
+    p.work = p.variant != awa::kVariantNarrow ? plan.work_wide : plan.work;
+    p.work_count = p.variant != awa::kVariantNarrow ? plan.work_wide_count : plan.work_count;
+    return AWA_OK;
+}
+
 bool valid_compute(int compute)
 {
     return compute == AWA_COMPUTE_F32 || compute == AWA_COMPUTE_BF16 || compute == AWA_COMPUTE_F32_MFMA;
@@ -707,14 +743,11 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
         return fail(AWA_ERR_INVALID, "invalid QKV input blobs");
     if (vl.head_dim != awa::kHeadDim || plan->rope_dim != awa::kRopeDim)
         return fail(AWA_ERR_INVALID, "fused path needs head_dim 128 and rope_dim 126; use the staged entry points");
-    // The kernel appends an identity row after the last coordinate.
+    // The kernel appends an identity row after the last coordinate, and its
+    // row table packs each row's three coordinates into 8-bit fields (below
+    // kMaxRopeCoords = 128).
     if (plan->rope_coords + 1 > awa::kMaxRopeCoords)
         return fail(AWA_ERR_INVALID, "RoPE coordinate range exceeds the fused kernel's table");
-    // Row table entries hold window-local coordinates in 10-bit fields, and
-    // the table itself lives in LDS next to the K/V tiles.
-    if (plan->window_t >= 1024 || plan->window_h >= 1024 || plan->window_w >= 1024 ||
-        plan->max_window_tokens > awa::kMaxFusedWindowTokens)
-        return fail(AWA_ERR_INVALID, "window too large for the fused kernel; use the staged entry points");
     const int elem = video_qkv->elemsize;
     const int align_elems = 16 / elem;
     if (!aligned16(video_qkv->data) || !aligned16(text_qkv->data) || vl.token_stride % align_elems ||
@@ -783,12 +816,11 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
         p.norm_eps = norm->eps;
     }
     p.windows = plan->dev.windows;
-    p.variant = attention_variant(compute, *plan);
-    p.work = p.variant != awa::kVariantNarrow ? plan->work_wide : plan->work;
-    p.work_count = p.variant != awa::kVariantNarrow ? plan->work_wide_count : plan->work_count;
     p.rope_cs = plan->dev.rope_cs;
     p.rope_coords = plan->rope_coords;
     p.max_window_tokens = plan->max_window_tokens;
+    if ((rc = launch_variant(compute, *plan, p)) != AWA_OK)
+        return rc;
     p.heads = vl.heads;
     p.text_tokens = plan->text_tokens;
     p.source_h = plan->source_h;
@@ -917,11 +949,11 @@ int awa_window_attention(const awa_plan* plan, const awa_blob* input, const awa_
     p.packed_out = static_cast<float*>(output->data);
     p.packed_out_row = output->cstep;
     p.windows = plan->dev.windows;
-    // Same variant choice as the fused layer, so that both give the same bits.
-    p.variant = attention_variant(compute, *plan);
-    p.work = p.variant != awa::kVariantNarrow ? plan->work_wide : plan->work;
-    p.work_count = p.variant != awa::kVariantNarrow ? plan->work_wide_count : plan->work_count;
     p.max_window_tokens = plan->max_window_tokens;
+    // Same variant choice as the fused layer, so that both give the same bits
+    // (the packed layer's tables are smaller, so it fits wherever that does).
+    if ((rc = launch_variant(compute, *plan, p)) != AWA_OK)
+        return rc;
     p.heads = heads;
     p.text_tokens = plan->text_tokens;
     p.source_h = plan->source_h;

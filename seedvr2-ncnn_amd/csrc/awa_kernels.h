@@ -19,7 +19,11 @@ constexpr int kVariantNarrow = 0;   // 4 waves, single-buffered tiles
 constexpr int kVariantWidePipe = 1; // 8 waves, double-buffered, software-pipelined
 constexpr int kVariantWide = 2;     // 8 waves, single-buffered tiles (the narrow loop on 256 rows)
 constexpr int kMaxRopeCoords = 128; // RoPE coordinates the fused kernel holds in LDS
-constexpr int kMaxFusedWindowTokens = 1536; // rows of the fused kernel's LDS row table
+// Windows the attention kernels accept: fewer rows than this (the float
+// reciprocal row decode is exact below it), and LDS tiles + tables within a
+// workgroup's share of a CU's LDS.
+constexpr int kMaxWindowRows = 1 << 14;
+constexpr size_t kWorkgroupLds = 160 * 1024;
 
 // One QKV source: row of (token, qkv, head) starts at
 // token * token_stride + qkv * qkv_stride + head * head_dim.
@@ -73,6 +77,10 @@ struct AttentionLaunch
 };
 
 hipError_t launch_attention(const AttentionLaunch& p, hipStream_t stream);
+// LDS of one workgroup of that kernel: the static K/V tiles of the variant
+// (bf16 or fp32 MFMA) and the dynamic norm / RoPE / row tables of a launch.
+size_t attention_static_lds(bool bf16_mfma, int variant);
+size_t attention_dynamic_lds(const AttentionLaunch& p);
 
 // fp32 window attention with nearly exact scores: Q/K as int8 digit slices
 // on int8 MFMA (exact int32 sums), P V as bf16 pieces on bf16 MFMA

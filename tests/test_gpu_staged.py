@@ -90,6 +90,34 @@ def test_window_attention_packed(gpu, compute, shifted):
         assert rel_err(got, ref) <= 2e-2
 
 
+def test_staged_chain_production_window(gpu):
+    """The four staged layers at the production 121-frame 720p geometry:
+    latent 31 x 45 x 80, windows (4, 3, 3) of up to 8 x 15 x 27 video tokens,
+    58 text tokens: 3298-row windows (the fp32 kernel's 4-wave form)."""
+    g = geometry((31, 45, 80, 4, 3, 3, 58), False)
+    print("case staged chain 31x45x80 (4,3,3) text 58", flush=True)
+    heads = 1
+    video, text = qkv_inputs(g, heads, HEAD_DIM, 20260914)
+    plan = make_plan(g)
+    assert plan.info.max_window_tokens == 8 * 15 * 27 + 58
+    S = plan.info.sequence_tokens
+    vq, tq = qkv_blob(video, "a", 4), qkv_blob(text, "a", 4)
+    packed = mat3(HEAD_DIM, 3 * heads, S, 4)
+    cu = DeviceMat(dict(w=plan.info.window_count + 1, dims=1), plan.info.window_count + 1, 4)
+    roped = mat3(HEAD_DIM, 3 * heads, S, 4)
+    att = mat3(HEAD_DIM, heads, S, 4)
+    vo = video_out_blob(g.t, g.h, g.w, heads, HEAD_DIM, 4, False)
+    to = mat3(HEAD_DIM, heads, g.text_tokens, 4)
+    plan.pack(vq.blob, tq.blob, packed.blob, cu.blob)
+    plan.mmrope(packed.blob, roped.blob)
+    plan.window_attention(roped.blob, att.blob, A.COMPUTE_F32)
+    plan.unpack(att.blob, vo.blob, to.blob)
+    A.synchronize()
+    ref_v, ref_t = O.awa_layer(g, video, text, heads, HEAD_DIM)
+    assert abs_err(read_video(vo, g.t, g.h, g.w, heads, HEAD_DIM), ref_v) <= 1e-4
+    assert abs_err(read_mat3(to), ref_t) <= 1e-4
+
+
 @pytest.mark.parametrize("head_dim", [8, 40])
 def test_window_attention_generic_head_dim(gpu, head_dim):
     g = geometry((2, 6, 6, 1, 2, 2, 3), True)
