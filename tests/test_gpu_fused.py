@@ -94,6 +94,29 @@ def test_production_single_window(gpu):
     assert abs_err(got_t, ref_t) <= FP32_ATOL
 
 
+# The reference's production window setting (4, 3, 3) with 58 text tokens on
+# the 720p latent grid (45 x 80): 13 latent frames give windows of 4 x 15 x
+# 27 video tokens, 1678 rows with the text (tools/reference/dit_stack.py:20).
+@pytest.mark.parametrize("shifted", [False, True])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_production_720p_windows(gpu, shifted, bf16):
+    g = geometry((13, 45, 80, 4, 3, 3, 58), shifted)
+    print(f"case 13x45x80 (4,3,3) text 58 shifted={shifted} bf16={bf16}", flush=True)
+    heads = 2
+    plan = A.Plan(A.LayerParams(*g.args, g.text_tokens, g.shifted))
+    assert plan.info.max_window_tokens == 4 * 15 * 27 + 58
+    video, text = qkv_inputs(g, heads, HEAD_DIM, 20260913)
+    if bf16:
+        video, text = bf16_round(video), bf16_round(text)
+    ref_v, ref_t = O.awa_layer(g, video, text, heads, HEAD_DIM)
+    if bf16:
+        got_v, got_t = run_fused(g, video, text, A.COMPUTE_BF16, in_elem=2, out_elem=2)
+        assert rel_err(got_v, ref_v) <= BF16_RTOL and rel_err(got_t, ref_t) <= BF16_RTOL
+    else:
+        got_v, got_t = run_fused(g, video, text, A.COMPUTE_F32)
+        assert abs_err(got_v, ref_v) <= FP32_ATOL and abs_err(got_t, ref_t) <= FP32_ATOL
+
+
 @pytest.mark.parametrize("layout", ["a", "b", "c", "d"])
 @pytest.mark.parametrize("batch_out", [False, True])
 def test_layouts_identical(gpu, layout, batch_out):
@@ -154,7 +177,7 @@ def test_bf16_output_rounding(gpu):
 @pytest.mark.parametrize("shifted", [False, True])
 @pytest.mark.parametrize("bf16", [False, True])
 def test_benchmark_shapes(gpu, name, shifted, bf16):
-    heads = 20 if name == "clip_9x16x16" else 4
+    heads = 20
     g = geometry(CONFIGS[name], shifted)
     print(f"case {name} shifted={shifted} bf16={bf16} heads={heads}", flush=True)
     video, text = qkv_inputs(g, heads, HEAD_DIM, 20260825)
@@ -190,9 +213,9 @@ def test_precision_combinations(gpu, in_elem, out_elem, compute):
 
 
 def test_text_mean_repeated_launches(gpu):
-    """The in-launch text mean leaves its counters ready for the next launch:
-    one plan run repeatedly, in both arithmetics and with the head count
-    changing between runs, gives the same bits every time."""
+    """The plan's lazily rebuilt work lists and text-row workspace give the
+    same bits on repeated launches of one plan, in both arithmetics and with
+    the head count changing between runs."""
     g = geometry(RAGGED[1], True)
     print(f"case repeated launches {RAGGED[1]} shifted", flush=True)
     plan = A.Plan(A.LayerParams(*g.args, g.text_tokens, g.shifted))
