@@ -4,6 +4,7 @@
 // (:1237-1291); the device work is the C ABI's.
 #include "awa_layers.h"
 
+#include <algorithm>
 #include <cerrno>
 #include <cstdint>
 #include <cstdio>
@@ -457,6 +458,231 @@ const ParamLayer* Net::find_layer(const std::string& name) const
         if (l.name == name)
             return &l;
     return nullptr;
+}
+
+int Net::load_model(const Option& opt)
+{
+    opt_ = opt;
+    for (ParamLayer& l : layers_)
+        if (l.layer && (l.layer->upload_model(opt) != 0 || l.layer->create_pipeline(opt) != 0))
+        {
+            error_ = "upload_model / create_pipeline failed for layer " + l.name + " (" + l.type + ")";
+            return -1;
+        }
+    return 0;
+}
+
+Extractor Net::create_extractor() const
+{
+    return Extractor(this);
+}
+
+namespace
+{
+
+// ncnn Reshape::forward for the shapes a DiT block uses: the output extents
+// from params 0 (w), 1 (h), 11 (d), 2 (c), -1 inferred from the element
+// count, 0 keeping the input's extent, dims set by the last given param.
+// Dense inputs are reshaped in place (a view); inputs with channel or batch
+// padding (the NCNN_BATCH video layout) are first copied dense on the device.
+int reshape_forward(const ParamDict& pd, const Mat& in, Mat& out, const Option& opt, std::string& error)
+{
+    constexpr int kUnset = -233;
+    const long long plane = static_cast<long long>(in.w) * in.h * in.d;
+    const long long total = plane * in.c * in.n;
+    int ext[4] = {pd.get(0, kUnset), pd.get(1, kUnset), pd.get(11, kUnset), pd.get(2, kUnset)}; // w h d c
+    const int dims = ext[2] != kUnset ? 4 : ext[3] != kUnset ? 3 : ext[1] != kUnset ? 2 : 1;
+    const int in_ext[4] = {in.w, in.h, in.d, in.c};
+    const int used[4] = {1, dims >= 2, dims == 4, dims >= 3};
+    long long known = 1;
+    int infer = -1;
+    for (int i = 0; i < 4; i++)
+    {
+        if (!used[i])
+        {
+            ext[i] = 1;
+            continue;
+        }
+        if (ext[i] == 0)
+            ext[i] = in_ext[i];
+        if (ext[i] == -1)
+        {
+            if (infer >= 0)
+            {
+                error = "Reshape with more than one -1 extent";
+                return -1;
+            }
+            infer = i;
+            continue;
+        }
+        if (ext[i] <= 0)
+        {
+            error = "Reshape extent " + std::to_string(ext[i]) + " is invalid";
+            return -1;
+        }
+        known *= ext[i];
+    }
+    if (infer >= 0)
+    {
+        if (known == 0 || total % known != 0)
+        {
+            error = "Reshape cannot infer an extent";
+            return -1;
+        }
+        ext[infer] = static_cast<int>(total / known);
+        known *= ext[infer];
+    }
+    if (known != total)
+    {
+        error = "Reshape to " + std::to_string(known) + " elements from " + std::to_string(total);
+        return -1;
+    }
+    const long long out_plane = static_cast<long long>(ext[0]) * ext[1] * ext[2];
+    if (dims >= 3 && (out_plane * static_cast<long long>(in.elemsize)) % 16 != 0)
+    {
+        error = "Reshape to a padded channel layout is not supported";
+        return -1;
+    }
+    // A dense copy of the input (same shape, no channel or batch padding).
+    Mat dense = in;
+    const bool padded = (in.dims >= 3 && in.cstep != plane) || (in.n > 1 && in.nstep != plane * in.c);
+    if (padded)
+    {
+        Mat flat;
+        if (flat.create(static_cast<int>(total), in.elemsize, opt.blob_allocator) != 0)
+        {
+            error = "Reshape copy allocation failed";
+            return -100;
+        }
+        awa_blob dst = in.blob();
+        dst.data = flat.data;
+        dst.cstep = plane;
+        dst.nstep = plane * in.c;
+        const awa_blob src = in.blob();
+        if (awa_cast(&src, &dst, opt.stream) != AWA_OK)
+        {
+            error = std::string("Reshape copy: ") + awa_last_error();
+            return -1;
+        }
+        dense = flat;
+    }
+    out = dense;
+    out.dims = dims;
+    out.w = ext[0];
+    out.h = ext[1];
+    out.d = ext[2];
+    out.c = ext[3];
+    out.n = 1;
+    out.cstep = dims >= 3 ? out_plane : out_plane * ext[3];
+    out.nstep = out.cstep * ext[3];
+    return 0;
+}
+
+} // namespace
+
+int Extractor::input(const char* blob_name, const Mat& in)
+{
+    if (!blob_name || in.empty())
+    {
+        error_ = "input: null blob name or empty Mat";
+        return -1;
+    }
+    blobs_[blob_name] = in;
+    return 0;
+}
+
+int Extractor::run(const ParamLayer& l)
+{
+    std::vector<Mat> bottoms;
+    for (const std::string& b : l.bottoms)
+    {
+        const auto it = blobs_.find(b);
+        if (it == blobs_.end())
+        {
+            error_ = "layer " + l.name + " needs blob " + b + ", which is neither an input nor produced";
+            return -1;
+        }
+        bottoms.push_back(it->second);
+    }
+    std::vector<Mat> tops;
+    int rc = 0;
+    if (l.layer)
+        rc = l.layer->forward(bottoms, tops, net_->option());
+    else if (l.type == "Reshape" && bottoms.size() == 1 && l.tops.size() == 1)
+    {
+        tops.resize(1);
+        rc = reshape_forward(l.pd, bottoms[0], tops[0], net_->option(), error_);
+    }
+    else if (l.type == "Split" && bottoms.size() == 1)
+        tops.assign(l.tops.size(), bottoms[0]);
+    else
+    {
+        error_ = "layer " + l.name + " of type " + l.type + " is not run by this runtime";
+        return -1;
+    }
+    if (rc != 0 || tops.size() != l.tops.size())
+    {
+        if (error_.empty())
+            error_ = "layer " + l.name + " (" + l.type + ") failed: " + std::to_string(rc);
+        return rc != 0 ? rc : -1;
+    }
+    for (size_t i = 0; i < tops.size(); i++)
+        blobs_[l.tops[i]] = tops[i];
+    return 0;
+}
+
+int Extractor::extract(const char* blob_name, Mat& out)
+{
+    error_.clear();
+    if (!blob_name)
+    {
+        error_ = "extract: null blob name";
+        return -1;
+    }
+    const std::vector<ParamLayer>& layers = net_->layers();
+    // The layers the blob depends on, found backwards from its producer.
+    std::vector<char> needed(layers.size(), 0);
+    std::vector<std::string> wanted{blob_name};
+    while (!wanted.empty())
+    {
+        const std::string b = wanted.back();
+        wanted.pop_back();
+        if (blobs_.count(b))
+            continue;
+        bool found = false;
+        for (size_t i = 0; i < layers.size() && !found; i++)
+            for (const std::string& t : layers[i].tops)
+                if (t == b)
+                {
+                    found = true;
+                    if (!needed[i])
+                    {
+                        needed[i] = 1;
+                        wanted.insert(wanted.end(), layers[i].bottoms.begin(), layers[i].bottoms.end());
+                    }
+                }
+        if (!found)
+        {
+            error_ = "blob " + b + " is not produced by any layer";
+            return -1;
+        }
+    }
+    for (size_t i = 0; i < layers.size(); i++)
+    {
+        if (!needed[i] || std::all_of(layers[i].tops.begin(), layers[i].tops.end(),
+                                      [&](const std::string& t) { return blobs_.count(t) != 0; }))
+            continue;
+        if (layers[i].type == "Input")
+        {
+            error_ = "input blob " + (layers[i].tops.empty() ? std::string("?") : layers[i].tops[0]) + " was not set";
+            return -1;
+        }
+        const int rc = run(layers[i]);
+        if (rc != 0)
+            return rc;
+    }
+    out = blobs_.at(blob_name);
+    return 0;
 }
 
 } // namespace hip

@@ -158,6 +158,8 @@ struct ParamLayer
     int featmask = 0;             // ncnn Layer::featmask (param 31); bit 2 keeps a layer's storage fp32
 };
 
+class Extractor;
+
 // Custom-layer registry with ncnn::Net's register_custom_layer signature, and
 // ncnn::Net::load_param for the .param text format the reference's packages
 // use (magic 7767517, "layer_count blob_count", then one line per layer:
@@ -165,6 +167,8 @@ struct ParamLayer
 // tools/export_dit_block.py:38-124, :578-644; read by load_graph,
 // src/dit/dit_stack.cpp:167-220). Layers of registered types are created and
 // given their ParamDict; a layer's load_param failure fails the load.
+// load_model then uploads and creates the pipelines of the created layers
+// (the AWA layers carry no weights), and create_extractor runs the graph.
 class Net
 {
 public:
@@ -183,6 +187,12 @@ public:
     int blob_count() const { return blob_count_; }
     const std::string& last_error() const { return error_; }
 
+    // upload_model + create_pipeline of every created layer, with opt as the
+    // net's option (ncnn::Net::load_model's role here: no weight file).
+    int load_model(const Option& opt);
+    const Option& option() const { return opt_; }
+    Extractor create_extractor() const;
+
 private:
     struct Entry
     {
@@ -192,6 +202,29 @@ private:
     std::map<std::string, Entry> registry_;
     std::vector<ParamLayer> layers_;
     int blob_count_ = 0;
+    std::string error_;
+    Option opt_;
+};
+
+// Runs a loaded net the way ncnn::Extractor does: input() binds blobs by
+// name (the Input layers' tops), extract() runs the layers the requested blob
+// depends on, in file order, and returns it. Runs the created layers and
+// ncnn's Reshape (params 0 = w, 1 = h, 11 = d, 2 = c; -1 inferred, 0 keeps
+// the input's extent; padded inputs are first copied dense, as ncnn's Reshape
+// does with a flattened copy); a needed layer of any other type fails the
+// extraction with -1. Enqueued on the net option's stream.
+class Extractor
+{
+public:
+    explicit Extractor(const Net* net) : net_(net) {}
+    int input(const char* blob_name, const Mat& in);
+    int extract(const char* blob_name, Mat& out);
+    const std::string& last_error() const { return error_; }
+
+private:
+    int run(const ParamLayer& layer);
+    const Net* net_;
+    std::map<std::string, Mat> blobs_;
     std::string error_;
 };
 

@@ -12,6 +12,13 @@
 //       Seeded inputs on device 0, the four-layer chain and the fused chain;
 //       writes inputs and outputs as float32 files into OUTDIR and prints the
 //       largest staged-vs-fused difference.
+//   awa_layers_check paramforward OUTDIR t h w nt nh nw text shifted heads bf16 dynamic batch
+//       A DiT block's AWA section as .param text (static grid, or the
+//       dynamic 0=-1 1=-1 2=-1 template with a runtime spec), loaded with
+//       Net::load_param_mem and Net::load_model and run by an Extractor on
+//       seeded inputs, the Unpack video output in the NCNN_BATCH layout when
+//       batch is 1; writes the inputs, the reshaped video matrix
+//       (awa_video_batch) and the text output as float32 files into OUTDIR.
 //   awa_layers_check dit
 //       Host-only checks of the DiT precision layers (DitRMSNorm,
 //       DitQKVConcat): registration, params, and
@@ -128,6 +135,28 @@ std::string block_param(const char* t, const char* h, const char* w, int shifted
            "SeedVR2AWAUnpack awa_unpack 1 2 attended vid_out txt_out " + grid + rest + "\n"
            "Reshape reshape_awa_video_batch 1 1 vid_out awa_video_batch 0=2560 1=-1\n"
            "Gemm gemm_0 1 1 awa_video_batch proj 10=-1 2=0 3=1 4=0 5=1 6=1 7=0 8=2560 9=2560 -23310=3,1.0,0.5,-2\n";
+}
+
+// The same section for any grid and head count: grid strings "-1" give the
+// dynamic template, whose video batch reshape infers its height (1=-1).
+std::string block_param_for(const std::string& t, const std::string& h, const std::string& w, int nt, int nh, int nw,
+                            int text, int shifted, int heads, long long tokens, bool dynamic)
+{
+    const std::string grid = "0=" + t + " 1=" + h + " 2=" + w;
+    const std::string rest = " 3=" + std::to_string(nt) + " 4=" + std::to_string(nh) + " 5=" + std::to_string(nw) +
+                             " 6=" + std::to_string(text) + " 7=" + std::to_string(shifted);
+    const std::string hidden = std::to_string(heads * 128);
+    return "7767517\n"
+           "8 10\n"
+           "Input in0 0 1 vid_qkv 0=128 1=" + std::to_string(3 * heads) + " 2=" + std::to_string(tokens) + "\n"
+           "Input in1 0 1 txt_qkv 0=128 1=" + std::to_string(3 * heads) + " 2=" + std::to_string(text) + "\n"
+           "SeedVR2AWAPack awa_pack 2 2 vid_qkv txt_qkv packed awa_cu_seqlens " + grid + rest + "\n"
+           "SeedVR2MMRoPE mmrope 1 1 packed roped " + grid + rest + " 8=126\n"
+           "SeedVR2WindowAttention awa_attention 1 1 roped attended " + grid + rest + "\n"
+           "SeedVR2AWAUnpack awa_unpack 1 2 attended vid_out txt_out " + grid + rest + "\n"
+           "Reshape reshape_awa_video_batch 1 1 vid_out awa_video_batch 0=" + hidden + " 1=" +
+           (dynamic ? std::string("-1") : std::to_string(tokens)) + "\n"
+           "Gemm gemm_0 1 1 awa_video_batch proj 10=-1 2=0 3=1 4=0 5=1 6=1 7=0 8=" + hidden + " 9=" + hidden + "\n";
 }
 
 int run_param()
@@ -319,6 +348,76 @@ int run_forward(int argc, char** argv)
     for (auto* layer : {pack.get(), rope.get(), attention.get(), unpack.get()})
         layer->destroy_pipeline(opt);
     std::printf("forward: staged vs fused max abs diff %.9g\n", diff);
+    return 0;
+}
+
+int run_param_forward(int argc, char** argv)
+{
+    if (argc < 15)
+    {
+        std::fprintf(stderr, "usage: paramforward OUTDIR t h w nt nh nw text shifted heads bf16 dynamic batch\n");
+        return 2;
+    }
+    const std::string dir = argv[2];
+    int a[12];
+    for (int i = 0; i < 12; i++)
+        a[i] = std::atoi(argv[3 + i]);
+    const int t = a[0], h = a[1], w = a[2], text = a[6], heads = a[8];
+    const bool bf16 = a[9] != 0, dynamic = a[10] != 0, batch = a[11] != 0;
+    const int n = t * h * w, d = 128;
+    const size_t es = bf16 ? 2 : 4;
+    if (awa_runtime_init(0) != AWA_OK)
+    {
+        std::fprintf(stderr, "no device: %s\n", awa_last_error());
+        return 1;
+    }
+    const std::string text_param =
+        dynamic ? block_param_for("-1", "-1", "-1", a[3], a[4], a[5], text, a[7], heads, n, true)
+                : block_param_for(std::to_string(t), std::to_string(h), std::to_string(w), a[3], a[4], a[5], text,
+                                  a[7], heads, n, false);
+    seedvr2::AwaRuntimeSpec spec{t, h, w, n};
+    Net net;
+    register_seedvr2_awa_layers(net, dynamic ? &spec : nullptr);
+    Option opt;
+    opt.use_bf16_storage = bf16;
+    opt.use_batch_video_layout = batch;
+    if (net.load_param_mem(text_param.c_str()) != 0 || net.load_model(opt) != 0)
+    {
+        std::fprintf(stderr, "load failed: %s\n", net.last_error().c_str());
+        return 1;
+    }
+    Mat video, txt;
+    if (video.create(d, 3 * heads, n, es, nullptr) != 0 || txt.create(d, 3 * heads, text, es, nullptr) != 0)
+        return 1;
+    awa_fill_normal(video.data, static_cast<size_t>(video.total()), static_cast<int>(es), 20260911ULL, nullptr);
+    awa_fill_normal(txt.data, static_cast<size_t>(txt.total()), static_cast<int>(es), 20260912ULL, nullptr);
+    seedvr2::hip::Extractor ex = net.create_extractor();
+    Mat vb, tt, proj;
+    if (ex.input("vid_qkv", video) != 0 || ex.input("txt_qkv", txt) != 0 || ex.extract("awa_video_batch", vb) != 0 ||
+        ex.extract("txt_out", tt) != 0 || awa_stream_synchronize(nullptr) != 0)
+    {
+        std::fprintf(stderr, "extract failed: %s %s\n", ex.last_error().c_str(), awa_last_error());
+        return 1;
+    }
+    if (vb.dims != 2 || vb.w != heads * d || vb.h != n || tt.dims != 3 || tt.w != d || tt.h != heads || tt.c != text)
+    {
+        std::fprintf(stderr, "unexpected shapes: video batch dims %d %dx%d, text dims %d\n", vb.dims, vb.w, vb.h, tt.dims);
+        return 1;
+    }
+    // The block's projection Gemm is not part of this runtime: extracting past it fails cleanly.
+    if (ex.extract("proj", proj) == 0 || ex.last_error().find("Gemm") == std::string::npos)
+    {
+        std::fprintf(stderr, "extracting the Gemm output should fail: %s\n", ex.last_error().c_str());
+        return 1;
+    }
+    if (!write_file(dir + "/video_qkv.f32", to_host_float(video)) || !write_file(dir + "/text_qkv.f32", to_host_float(txt)) ||
+        !write_file(dir + "/video_batch.f32", to_host_float(vb)) || !write_file(dir + "/text_out.f32", to_host_float(tt)))
+    {
+        std::fprintf(stderr, "cannot write into %s\n", dir.c_str());
+        return 1;
+    }
+    std::printf("paramforward: %s %dx%dx%d shifted=%d heads=%d bf16=%d batch=%d: video batch %dx%d\n",
+                dynamic ? "dynamic" : "static", t, h, w, a[7], heads, bf16, batch, vb.h, vb.w);
     return 0;
 }
 
@@ -531,6 +630,8 @@ int main(int argc, char** argv)
         return run_params();
     if (argc >= 2 && std::strcmp(argv[1], "forward") == 0)
         return run_forward(argc, argv);
+    if (argc >= 2 && std::strcmp(argv[1], "paramforward") == 0)
+        return run_param_forward(argc, argv);
     if (argc >= 2 && std::strcmp(argv[1], "param") == 0)
         return run_param();
     if (argc >= 2 && std::strcmp(argv[1], "dit") == 0)

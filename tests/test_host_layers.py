@@ -80,6 +80,48 @@ def test_layer_chain_matches_oracle(gpu, tmp_path, params, heads, bf16):
     assert diff <= (1e-6 if not bf16 else 1e-2)
 
 
+PARAM_FORWARD_CASES = [
+    # t, h, w, nt, nh, nw, text, shifted, heads, bf16, dynamic, batch video layout
+    ((2, 16, 16, 1, 8, 8, 64, 1), 4, 0, 0, 0),
+    ((2, 16, 16, 1, 8, 8, 64, 0), 4, 1, 1, 1),
+    ((9, 16, 16, 3, 8, 8, 64, 0), 4, 0, 1, 1),
+    ((9, 16, 16, 3, 8, 8, 64, 1), 4, 1, 0, 0),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("params,heads,bf16,dynamic,batch", PARAM_FORWARD_CASES)
+def test_param_package_runs_on_device(gpu, tmp_path, params, heads, bf16, dynamic, batch):
+    """A DiT block's AWA section as the reference export writes it
+    (tools/export_dit_block.py:578-644, :740-743; the dynamic template of
+    :38-124), loaded by Net::load_param_mem (static grid, or 0=-1 1=-1 2=-1
+    with the runtime spec), given its pipelines by Net::load_model and run by
+    an Extractor, as load_graph and DitStackSession::run drive the reference
+    package (src/dit/dit_stack.cpp:167-220, :951-963): Pack, MMRoPE,
+    WindowAttention, Unpack, then reshape_awa_video_batch's [N][H*d] view of
+    the video output (a dense copy of the NCNN_BATCH layout). Compared with
+    the oracle."""
+    print(f"param package case {params} heads={heads} bf16={bf16} dynamic={dynamic} batch={batch}", flush=True)
+    r = run_check("paramforward", str(tmp_path), *map(str, params), str(heads), str(bf16), str(dynamic), str(batch))
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0, r.stdout + r.stderr
+    t, h, w, nt, nh, nw, text, shifted = params
+    g = O.Geometry(t, h, w, nt, nh, nw, text, bool(shifted))
+    n, d = g.source_tokens, 128
+
+    def load(name, shape):
+        return np.fromfile(os.path.join(tmp_path, name), np.float32).reshape(shape)
+
+    ref_v, ref_t = O.awa_layer(g, load("video_qkv.f32", (n, 3, heads, d)), load("text_qkv.f32", (text, 3, heads, d)),
+                               heads, d)
+    v = load("video_batch.f32", (n, heads * d)).reshape(n, heads, d)
+    tt = load("text_out.f32", (text, heads, d))
+    if bf16:
+        assert rel_err(v, ref_v) <= 2e-2 and rel_err(tt, ref_t) <= 2e-2
+    else:
+        assert np.max(np.abs(v - ref_v)) <= 1e-4 and np.max(np.abs(tt - ref_t)) <= 1e-4
+
+
 @pytest.mark.gpu
 def test_shape_trace(gpu, tmp_path):
     """SEEDVR2_TRACE_OPS prints one line per layer blob, in the reference's format."""
