@@ -73,6 +73,7 @@ def cpu_baseline(sample_layers: int) -> dict:
         "value": step_flops / step_s / 1e12,
         "unit": "TFLOP/s",
         "cores": 1,
+        "host": host_cpu(),
         "kind": "port",
         "sample": (f"one unshifted and one shifted fp32 layer of this workload ({', '.join(f'{t:.2f}' for t in times)} s), "
                    f"single thread, reference CPU loop order; projected 32-block step {step_s * 1e3:.0f} ms"),
@@ -136,6 +137,148 @@ def qk_prologue(A, bufs, stream, iters: int = 20) -> dict:
         plan.destroy()
     res["data"] = "bf16 raw QKV projection of a bf16 block, gammas U(0.5, 1.5), eps 1e-5"
     return res
+
+
+def host_cpu() -> dict:
+    """The host the CPU baseline ran on: model name, logical CPUs, and the
+    CPUs this process may use."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count(), "usable_cpus": len(os.sched_getaffinity(0))}
+
+
+# The BASELINE workloads, each run as a stack of attention layers with even
+# layers unshifted and odd layers shifted: (latent t, h, w), window counts,
+# arithmetic, the layers the config is quoted on.
+CONFIGS = {
+    "cfg1_fp32_image_1x16x16": ((1, 16, 16), (1, 8, 8), "fp32", ("unshifted",)),
+    "cfg2_bf16_shifted_2x16x16": ((2, 16, 16), (1, 8, 8), "bf16", ("shifted",)),
+    "cfg3_mixed_9x16x16": ((9, 16, 16), (3, 8, 8), "mixed", ("unshifted", "shifted")),
+    "cfg4_bf16_9x32x32": ((9, 32, 32), (3, 8, 8), "bf16", ("unshifted", "shifted")),
+    "cfg5_bf16_31x16x16": ((31, 16, 16), (8, 8, 8), "bf16", ("unshifted", "shifted")),
+}
+MALL_BYTES = 256 * 1024 * 1024
+
+
+def config_measurements(A, stream, steps: int = 10, profile_steps: int = 5) -> dict:
+    """Every BASELINE config in two regimes. HBM-cold: every layer reads its
+    own inputs and the stack's inputs and outputs total at least 1 GiB (four
+    times the 256 MB Infinity Cache), so no layer finds its data cached.
+    MALL-warm: every layer of the stack reads the same inputs, which stay in
+    the Infinity Cache after the first. Per layer (median over the stack's
+    unshifted or shifted layers, HIP events around each): the attention
+    kernel and the whole layer (kernel + text mean), TFLOP/s, the share of
+    the bf16 MFMA peak and the roofline fraction (F/t) / min(P, AI * 8 TB/s)
+    with P the MFMA peak of the layer's arithmetic; and ms per 32-layer step."""
+    out = {}
+    for name, (grid, windows, arith, quoted) in CONFIGS.items():
+        t, h, w = grid
+        N = t * h * w
+        per_block = lambda es: (N + TEXT) * HEADS * HEAD_DIM * 4 * es
+        res = {"latent": list(grid), "window_counts": list(windows), "arithmetic": arith}
+        for regime in ("hbm_cold", "mall_warm"):
+            blocks = 32
+            if regime == "hbm_cold" and arith != "mixed":
+                need = -(-(4 * MALL_BYTES) // per_block(4 if arith == "fp32" else 2))
+                blocks = max(32, need + (need & 1))
+            prefix = {"fp32": blocks, "bf16": 0, "mixed": FP32_PREFIX}[arith]
+            stack = A.AttentionStack(t, h, w, *windows, TEXT, blocks, prefix, HEADS, HEAD_DIM)
+            keep, ptrs = [], [[], [], [], []]
+            shared = {}
+            for b in range(blocks):
+                es = 4 if b < prefix else 2
+                if regime == "mall_warm" and es in shared:
+                    bufs = shared[es]
+                else:
+                    bufs = [A.DeviceBuffer(N * 3 * HEADS * HEAD_DIM * es), A.DeviceBuffer(TEXT * 3 * HEADS * HEAD_DIM * es),
+                            A.DeviceBuffer(N * HEADS * HEAD_DIM * es), A.DeviceBuffer(TEXT * HEADS * HEAD_DIM * es)]
+                    bufs[0].fill_normal(N * 3 * HEADS * HEAD_DIM, es, 7000 + 2 * b, stream)
+                    bufs[1].fill_normal(TEXT * 3 * HEADS * HEAD_DIM, es, 7001 + 2 * b, stream)
+                    keep.append(bufs)
+                    shared[es] = bufs
+                for i in range(4):
+                    ptrs[i].append(bufs[i].ptr)
+            stream.synchronize()
+            for _ in range(3):
+                stack.run(*ptrs, stream)
+            e0, e1 = A.Event(), A.Event()
+            e0.record(stream)
+            for _ in range(steps):
+                stack.run(*ptrs, stream)
+            e1.record(stream)
+            stream.synchronize()
+            step_ms = e0.elapsed_ms(e1) / steps
+            stack.set_profiling(True)
+            att = np.zeros((profile_steps, blocks))
+            lay = np.zeros((profile_steps, blocks))
+            for s in range(profile_steps):
+                stack.run(*ptrs, stream)
+                stream.synchronize()
+                att[s], lay[s] = stack.block_times()
+            flops = stack.block_flops()
+            stack.destroy()
+            del keep, shared
+            entry = {"layers_in_stack": blocks,
+                     "ms_per_32_layers": round(step_ms * 32 / blocks, 4),
+                     "step_input_mb": round(sum(per_block(4 if b < prefix else 2) for b in range(blocks)) / 1e6
+                                            if regime == "hbm_cold" else 0.0, 1)}
+            for kind in quoted:
+                for label, precision in (("fp32", range(prefix)), ("bf16", range(prefix, blocks))):
+                    idx = np.array([b for b in precision if (b & 1) == (kind == "shifted")], dtype=int)
+                    if idx.size == 0:
+                        continue
+                    k_ms = float(np.median(att[:, idx]))
+                    l_ms = float(np.median(lay[:, idx]))
+                    fl = float(flops[idx].mean())
+                    es = 4 if label == "fp32" else 2
+                    alg = float(per_block(es))
+                    peak = PEAK_FP32 if label == "fp32" else PEAK_BF16
+                    roof = min(peak, fl / alg * PEAK_HBM)
+                    key = kind if arith != "mixed" else f"{label}_{kind}"
+                    entry[key] = {
+                        "kernel_ms": round(k_ms, 5), "layer_ms": round(l_ms, 5),
+                        "gflop": round(fl / 1e9, 3), "algorithmic_mb": round(alg / 1e6, 2),
+                        "tflops": round(fl / (k_ms * 1e-3) / 1e12, 2),
+                        "layer_tflops": round(fl / (l_ms * 1e-3) / 1e12, 2),
+                        "pct_bf16_peak": round(100.0 * fl / (k_ms * 1e-3) / PEAK_BF16, 2),
+                        "roofline_frac": round(fl / (k_ms * 1e-3) / roof, 4),
+                        "roof": "hbm" if roof < peak else ("mfma_fp32" if label == "fp32" else "mfma_bf16"),
+                    }
+            res[regime] = entry
+        out[name] = res
+    return out
+
+
+def cpu_baseline_cfg1() -> dict:
+    """The reference's CPU semantics on BASELINE's CPU-runnable case, the fp32
+    image layer (1x16x16, windows 1x8x8, 64 text tokens, 20 heads): the
+    oracle's single-threaded restatement of the CPU forward, whole layer."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    O.set_num_threads(1)
+    g = O.Geometry(1, 16, 16, 1, 8, 8, TEXT, False)
+    video = O.fill_gaussian(g.source_tokens * 3 * HEADS * HEAD_DIM, 20260823, 0).reshape(g.source_tokens, 3, HEADS,
+                                                                                      HEAD_DIM)
+    text = O.fill_gaussian(TEXT * 3 * HEADS * HEAD_DIM, 20260823, 1).reshape(TEXT, 3, HEADS, HEAD_DIM)
+    cu = O.build_maps(g).cu_seqlens
+    flops = float(sum(4.0 * (b - a) ** 2 * HEAD_DIM * HEADS for a, b in zip(cu[:-1], cu[1:])))
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        O.awa_layer(g, video, text, HEADS, HEAD_DIM, attention_order="cpu", text_order="cpu")
+        times.append(time.perf_counter() - t0)
+    s = float(np.median(times))
+    return {"ms_per_layer": round(s * 1e3, 2), "tflops": flops / s / 1e12, "cores": 1, "kind": "port",
+            "sample": "the whole fp32 image layer, median of 3 runs, single thread, reference CPU loop order",
+            "host": host_cpu()}
 
 
 MLP_HIDDEN = 6912  # SwiGLU hidden width for hidden 2560 (tools/reference/dit_block.py:195-197)
@@ -222,6 +365,8 @@ def main() -> int:
     ap.add_argument("--profile-steps", type=int, default=5, help="steps with per-block event timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dit-step", action="store_true", help="skip the full 32-block DiT step measurement")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the per-config table (every BASELINE config, HBM-cold and MALL-warm)")
     ap.add_argument("--dit-steps", type=int, default=5)
     ap.add_argument("--cpu-sample-layers", type=int, default=2, choices=(1, 2))
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "awa_attention_hbm_traffic.json"),
@@ -380,11 +525,14 @@ def main() -> int:
         },
     }
     result["qk_prologue"] = qk_prologue(A, buffers[FP32_PREFIX], stream)
+    del buffers, vq, tq, vo, to
+    if not args.no_configs:
+        result["configs"] = config_measurements(A, stream)
     if not args.no_dit_step:
-        del buffers, vq, tq, vo, to
         result["dit_step"] = dit_step(A, stream, args.dit_steps)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_sample_layers)
+        result["cpu_baseline_cfg1"] = cpu_baseline_cfg1()
     print(json.dumps(result), flush=True)
     stack.destroy()
     stream.destroy()
