@@ -45,6 +45,9 @@ namespace
 
 using namespace dev;
 
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
 // Variants (AttentionLaunch::variant):
 //   kVariantNarrow: 4 waves (128 query rows), single-buffered K/V tiles of 64
 //     (bf16) or 32 (fp32) keys, two barriers per tile; the LDS footprint stays
@@ -72,11 +75,13 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
     // 64-key tiles (two 32-key score blocks) on bf16 MFMA, 32 on fp32 MFMA.
     constexpr int KT = BF16 ? 64 : 32;
     constexpr int kKPitch = BF16 ? kHeadDim + 8 : kHeadDim + 4;
-    constexpr int kVPitch = BF16 ? KT + 8 : KT + 4;
+    // bf16: V row-major [key][feature] (pitch 160 elements: the transposed
+    // operand reads below hit distinct banks); fp32: V^T [feature][key].
+    constexpr int kVPitch = BF16 ? kHeadDim + 32 : KT + 4;
     constexpr int kElem = BF16 ? 2 : 4;
     constexpr int kRW = kRawWords8<TIn>;
     constexpr int kKBytes = KT * kKPitch * kElem;
-    constexpr int kVBytes = kHeadDim * kVPitch * kElem;
+    constexpr int kVBytes = (BF16 ? KT : kHeadDim) * kVPitch * kElem;
     constexpr int kBlocks = KT / 32; // 32-key score blocks per tile
 
     __shared__ __attribute__((aligned(16))) unsigned char k_lds[kBufs * kKBytes];
@@ -315,37 +320,46 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
     auto store_k = [&](int tile, int buf) { store_k_from(tile, buf, st.k); };
     auto store_v = [&](int buf) {
         unsigned char* const vb = v_lds + buf * kVBytes;
-        // V transposed: Vt[d][key], keys swizzled in groups of 8 per feature chunk.
-#pragma unroll
-        for (int j = 0; j < kVGroups; j++)
+        if constexpr (BF16)
         {
-        const int key = (kVKeys * (kr0 + kRowsPerPass * j)) ^ (8 * vt_swizzle<KT>(8 * kc));
-        const uint32_t* const sv = st.v + j * kVKeys * kRW;
+            // Row-major: each thread's 8 features of a key, one 16-byte store.
 #pragma unroll
-        for (int e = 0; e < 8; e++)
-        {
-            if constexpr (BF16)
-            {
-                // One word = (key, key+1) at feature 8kc + e.
-                const uint32_t* a = sv;
-                const uint32_t* b = sv + kRW;
-                uint32_t word;
-                if constexpr (sizeof(TIn) == 2)
-                    word = __builtin_amdgcn_perm(b[e >> 1], a[e >> 1], (e & 1) ? 0x07060302u : 0x05040100u);
-                else
-                    word = cvt_pk_bf16(__uint_as_float(a[e]), __uint_as_float(b[e]));
-                *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(vb) + (8 * kc + e) * kVPitch + key) = word;
-            }
-            else
-            {
-                float v;
-                if constexpr (sizeof(TIn) == 2)
-                    v = (e & 1) ? bf16_hi(sv[e >> 1]) : bf16_lo(sv[e >> 1]);
-                else
-                    v = __uint_as_float(sv[e]);
-                reinterpret_cast<float*>(vb)[(8 * kc + e) * kVPitch + key] = v;
-            }
+            for (int j = 0; j < kVGroups; j++)
+#pragma unroll
+                for (int i = 0; i < kVKeys; i++)
+                {
+                    const int key = kVKeys * (kr0 + kRowsPerPass * j) + i;
+                    const uint32_t* const sv = st.v + (j * kVKeys + i) * kRW;
+                    uint4 w;
+                    if constexpr (sizeof(TIn) == 2)
+                        w = make_uint4(sv[0], sv[1], sv[2], sv[3]);
+                    else
+                        w = make_uint4(cvt_pk_bf16(__uint_as_float(sv[0]), __uint_as_float(sv[1])),
+                                       cvt_pk_bf16(__uint_as_float(sv[2]), __uint_as_float(sv[3])),
+                                       cvt_pk_bf16(__uint_as_float(sv[4]), __uint_as_float(sv[5])),
+                                       cvt_pk_bf16(__uint_as_float(sv[6]), __uint_as_float(sv[7])));
+                    *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(vb) + key * kVPitch + 8 * kc) = w;
+                }
         }
+        else
+        {
+            // V transposed: Vt[d][key], keys swizzled in groups of 8 per feature chunk.
+#pragma unroll
+            for (int j = 0; j < kVGroups; j++)
+            {
+                const int key = (kVKeys * (kr0 + kRowsPerPass * j)) ^ (8 * vt_swizzle<KT>(8 * kc));
+                const uint32_t* const sv = st.v + j * kVKeys * kRW;
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                {
+                    float v;
+                    if constexpr (sizeof(TIn) == 2)
+                        v = (e & 1) ? bf16_hi(sv[e >> 1]) : bf16_lo(sv[e >> 1]);
+                    else
+                        v = __uint_as_float(sv[e]);
+                    reinterpret_cast<float*>(vb)[(8 * kc + e) * kVPitch + key] = v;
+                }
+            }
         }
     };
     auto store_tile = [&](int tile, int buf) {
@@ -651,21 +665,28 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
                         row_sum = __builtin_amdgcn_fdot2_f32_bf16(pair, ones, row_sum, false);
                     }
             }
-            // The four output chains are interleaved: consecutive MFMAs are
-            // independent. With d = 32 db + col (col < 32), 8 vt_swizzle(d)
-            // = 16 db + 8 (col / 16), so the swizzled column (8 half + 16 j)
-            // ^ 8 vt_swizzle(d) is a lane term, 8 (half ^ col / 16), plus
-            // (16 j) ^ (16 db): one lane base plus an immediate per read.
-            static_assert(KT == 64, "swizzle split for 64-key tiles");
-            const uint16_t* vt = reinterpret_cast<const uint16_t*>(v_lds + buf * kVBytes) + col * kVPitch +
-                                 8 * (half ^ (col >> 4));
+            // V^T operands read transposed from the row-major tile
+            // (ds_read_b64_tr_b16): within each group of 16 lanes, lane j
+            // addresses key row 8*half + j/4 (+4 for the second read) and
+            // features 16*(group & 1) + 4*(j & 3) of a 32-feature block, and
+            // receives column j of the 4 x 16 block its group read: keys
+            // 16 step + 8 half + [0, 8) of feature 32 db + col. The four
+            // output chains are interleaved: consecutive MFMAs are independent.
+            const uint16_t* vt = reinterpret_cast<const uint16_t*>(v_lds + buf * kVBytes) +
+                                 (8 * half + ((lane & 15) >> 2)) * kVPitch + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 #pragma unroll
             for (int j = 0; j < 2 * kBlocks; j++)
             {
                 bf16x8 va[4];
 #pragma unroll
                 for (int db = 0; db < 4; db++)
-                    va[db] = *reinterpret_cast<const bf16x8*>(vt + db * 32 * kVPitch + ((16 * j) ^ (16 * db)));
+                {
+                    const uint16_t* const base = vt + 16 * j * kVPitch + 32 * db;
+                    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base));
+                    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + 4 * kVPitch));
+                    const i16x4 lohi[2] = {lo, hi};
+                    va[db] = __builtin_bit_cast(bf16x8, lohi);
+                }
 #pragma unroll
                 for (int db = 0; db < 4; db++)
                     o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[db], pb[j], o[db], 0, 0, 0);
@@ -821,7 +842,7 @@ size_t attention_static_lds(bool bf16_mfma, int variant)
 {
     // K tile (keys x padded head_dim) and transposed V tile (head_dim x padded
     // keys): 64 bf16 keys or 32 fp32 keys; double-buffered in the pipeline.
-    const size_t tiles = bf16_mfma ? 64 * (kHeadDim + 8) * 2 + kHeadDim * (64 + 8) * 2
+    const size_t tiles = bf16_mfma ? 64 * (kHeadDim + 8) * 2 + 64 * (kHeadDim + 32) * 2
                                    : 32 * (kHeadDim + 4) * 4 + kHeadDim * (32 + 4) * 4;
     return (variant == kVariantWidePipe ? 2 : 1) * tiles;
 }
