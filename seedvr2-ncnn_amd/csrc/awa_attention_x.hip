@@ -5,16 +5,17 @@
 // because real-model Q/K make the scores large and cancelling. This kernel
 // computes the scores nearly exactly and rounds them once, on int8 MFMA:
 //
-// - Every Q row and K row is written as x = 2^(e-6) (d1 + d2 2^-7 + d3 2^-14
-//   + d4 2^-21) with e the row's exponent (max |x| < 2^e) and d1..d4 signed
-//   7-bit digits (int8 slices). The representation error is below 2^-28 of
-//   the row maximum.
-// - q.k = 2^(eq+ek-12) (C2 + C3 2^-7 + C4 2^-14 + C5 2^-21), where C_w sums
+// - Every Q row and K row is written as x = 2^(e-6) (d1 + d2 2^-8 + d3 2^-16
+//   + d4 2^-24) with e the row's exponent (max |x| < 2^e), d1 in [-64, 64] and
+//   d2..d4 in [-128, 127] (balanced base-256 digits, int8 slices). The
+//   representation error is below 2^-30 of the row maximum.
+// - q.k = 2^(eq+ek-12) (C2 + C3 2^-8 + C4 2^-16 + C5 2^-24), where C_w sums
 //   the slice products d_s(q) d_t(k) with s + t = w over the 128 features.
 //   v_mfma_i32_32x32x32_i8 accumulates them in int32 exactly (each C_w stays
-//   below 2^21), the dropped classes w > 5 weigh below 2^-28, and the classes
-//   are combined in fp32 from the smallest up, so a score carries about one
-//   fp32 rounding, like a compensated sum.
+//   below 2^23, so its conversion to fp32 is exact too), the dropped classes
+//   w > 5 weigh below 2^-30, and the classes are combined in fp32 from the
+//   smallest up, so a score carries one fp32 rounding, like a correctly
+//   rounded dot product.
 // - P V runs on bf16 MFMA with P = p1 + p2 + p3 and V = v1 + v2 + v3, three
 //   bf16 pieces each (all 24 bits of the fp32 value), products p1 (v1 + v2 +
 //   v3) + p2 (v1 + v2) + p3 v1 (the dropped ones weigh below 2^-24), fp32
@@ -57,44 +58,39 @@ constexpr int kXKSlice = kXKeys * kXKPitch;
 constexpr int kXVPitch = 160;    // bf16 elements per key row of one V slice (conflict-free transposed reads)
 constexpr int kXVSlice = kXKeys * kXVPitch * 2;
 
-// x ~= 2^(e-6) (d1 + d2 2^-7 + d3 2^-14 + d4 2^-21) for |x| < 2^e: x * 2^(27-e)
-// rounded to an integer X (|X| <= 2^27), then signed base-128 digits taken
-// from the bottom (d4, d3, d2 in [-64, 63], d1 in [-64, 64]).
-__device__ __forceinline__ void split_digits(float x, int e, int (&d)[4])
+// x ~= 2^(e-6) (d1 + d2 2^-8 + d3 2^-16 + d4 2^-24) for |x| < 2^e: X = x *
+// 2^(30-e) truncated (|X| < 2^30) plus 128 (1 + 2^8 + 2^16), so that its top
+// byte (arithmetic) is d1 and each lower byte b is a digit b - 128, the int8
+// b ^ 0x80.
+__device__ __forceinline__ uint32_t digit_word(float x, int e)
 {
-    int X = __float2int_rn(ldexpf(x, 27 - e));
-    const int d4 = (X << 25) >> 25;
-    X = (X - d4) >> 7;
-    const int d3 = (X << 25) >> 25;
-    X = (X - d3) >> 7;
-    const int d2 = (X << 25) >> 25;
-    d[0] = (X - d2) >> 7;
-    d[1] = d2;
-    d[2] = d3;
-    d[3] = d4;
+    return static_cast<uint32_t>(static_cast<int>(ldexpf(x, 30 - e))) + 0x808080u;
 }
 
-// Low bytes of four int32 as one word (byte i = x_i).
-__device__ __forceinline__ uint32_t pack_bytes(int x0, int x1, int x2, int x3)
+// The digits of four values as four int8 slices (w0 = d1 ... w3 = d4, byte i
+// from value i): a 4 x 4 byte transpose in eight v_perm_b32.
+__device__ __forceinline__ void transpose_digits(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3,
+                                                 uint32_t& w0, uint32_t& w1, uint32_t& w2, uint32_t& w3)
 {
-    const uint32_t lo = __builtin_amdgcn_perm(static_cast<uint32_t>(x1), static_cast<uint32_t>(x0), 0x0c0c0400u);
-    const uint32_t hi = __builtin_amdgcn_perm(static_cast<uint32_t>(x3), static_cast<uint32_t>(x2), 0x0c0c0400u);
-    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+    const uint32_t a = __builtin_amdgcn_perm(x1, x0, 0x06020400u); // x0.b0 x1.b0 x0.b2 x1.b2
+    const uint32_t b = __builtin_amdgcn_perm(x1, x0, 0x07030501u); // x0.b1 x1.b1 x0.b3 x1.b3
+    const uint32_t c = __builtin_amdgcn_perm(x3, x2, 0x06020400u);
+    const uint32_t d = __builtin_amdgcn_perm(x3, x2, 0x07030501u);
+    w0 = __builtin_amdgcn_perm(d, b, 0x07060302u);
+    w1 = __builtin_amdgcn_perm(c, a, 0x07060302u) ^ 0x80808080u;
+    w2 = __builtin_amdgcn_perm(d, b, 0x05040100u) ^ 0x80808080u;
+    w3 = __builtin_amdgcn_perm(c, a, 0x05040100u) ^ 0x80808080u;
 }
 
 // Eight consecutive values of one row as four int8 slices (two words each).
 __device__ __forceinline__ void split8(const float* v, int e, uint32_t (&w)[4][2])
 {
-    int d[8][4];
+    uint32_t x[8];
 #pragma unroll
     for (int i = 0; i < 8; i++)
-        split_digits(v[i], e, d[i]);
-#pragma unroll
-    for (int s = 0; s < 4; s++)
-    {
-        w[s][0] = pack_bytes(d[0][s], d[1][s], d[2][s], d[3][s]);
-        w[s][1] = pack_bytes(d[4][s], d[5][s], d[6][s], d[7][s]);
-    }
+        x[i] = digit_word(v[i], e);
+    transpose_digits(x[0], x[1], x[2], x[3], w[0][0], w[1][0], w[2][0], w[3][0]);
+    transpose_digits(x[4], x[5], x[6], x[7], w[0][1], w[1][1], w[2][1], w[3][1]);
 }
 
 // Three bf16 pieces of v (v1 = rne(v), v2 = rne(v - v1), v3 = rne(v - v1 - v2)),
@@ -428,10 +424,9 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
     // j of the 4 x 16 block its group read.
     const int vt_lane = (8 * half + ((lane & 15) >> 2)) * kXVPitch + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-    // Per-wave work on the tile in buffer buf, in two parts so that the next
-    // tile's K staging can be issued between them: (a) the weight classes 5
-    // and 4 of the scores, (b) classes 3 and 2, softmax, P and PV.
-    auto scores_a = [&](int buf, f32x16& f) {
+    // Per-wave work on the tile in buffer buf: (a) the score classes 5 and 4,
+    // (b) classes 3 and 2, both combined into f; (c) softmax, P and PV.
+    auto scores_hi = [&](int buf, f32x16& f) {
         const unsigned char* const kb = k_lds + buf * kKBuf + col * kXKPitch + 16 * half;
         // ---- scores: S^T = K Q^T, four exact int32 classes ----
         {
@@ -453,10 +448,10 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
             }
 #pragma unroll
             for (int i = 0; i < 16; i++)
-                f[i] = fmaf(static_cast<float>(c5[i]), 1.f / 128.f, static_cast<float>(c4[i]));
+                f[i] = fmaf(static_cast<float>(c5[i]), 1.f / 256.f, static_cast<float>(c4[i]));
         }
     };
-    auto finish = [&](int tile, int buf, f32x16& f) {
+    auto scores_lo = [&](int buf, f32x16& f) {
         const unsigned char* const kb = k_lds + buf * kKBuf + col * kXKPitch + 16 * half;
         {
             i32x16 c3 = izero, c2 = izero;
@@ -472,10 +467,12 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
 #pragma unroll
             for (int i = 0; i < 16; i++)
             {
-                f[i] = fmaf(f[i], 1.f / 128.f, static_cast<float>(c3[i]));
-                f[i] = fmaf(f[i], 1.f / 128.f, static_cast<float>(c2[i]));
+                f[i] = fmaf(f[i], 1.f / 256.f, static_cast<float>(c3[i]));
+                f[i] = fmaf(f[i], 1.f / 256.f, static_cast<float>(c2[i]));
             }
         }
+    };
+    auto softmax_pv = [&](int tile, int buf, const f32x16& f, bool last) {
         // Register i holds key 16*(i/8) + 8*half + i%8 (key-permuted K rows).
         float kq[16];
         {
@@ -490,7 +487,7 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
 #pragma unroll
         for (int i = 0; i < 16; i++)
             s[i] = fmaf(f[i], kq[i], -row_max);
-        if (tile == tiles - 1 && (L % KT))
+        if (last && (L % KT))
         {
             const int key0 = tile * KT + 8 * half;
 #pragma unroll
@@ -583,9 +580,13 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
 
     if constexpr (WIDE)
     {
-        // Step t: (a) of tile t, K(t+1) into the other buffer, (b) of tile t,
-        // V(t+1), then the loads of tile t+2; one barrier. A buffer is
-        // rewritten only after the barrier that ends the step reading it.
+        // Step t: the scores, softmax and PV of tile t, the staging of tile
+        // t+1 (K and V into the other buffer), the loads of tile t+2, one
+        // barrier. A buffer is rewritten only after the barrier that ends the
+        // step reading it. Waves 0-3 compute first and stage last, waves 4-7
+        // (the second wave on each SIMD) stage first, so that one wave's VALU
+        // staging runs while the other's MFMAs hold the matrix core.
+        const bool stage_first = wave >= 4;
         store_k(0, 0);
         store_v(0);
         if (tiles > 1)
@@ -595,19 +596,26 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
         {
             const int buf = tile & 1;
             const bool next = tile + 1 < tiles;
-            f32x16 f;
+            auto stage = [&]() {
+                if (next)
+                {
+                    store_k(tile + 1, buf ^ 1);
+                    store_v(buf ^ 1);
+                    if (tile + 2 < tiles)
+                        load_tile(tile + 2);
+                }
+            };
+            if (stage_first)
+                stage();
             if (wave_active)
-                scores_a(buf, f);
-            if (next)
-                store_k(tile + 1, buf ^ 1);
-            if (wave_active)
-                finish(tile, buf, f);
-            if (next)
             {
-                store_v(buf ^ 1);
-                if (tile + 2 < tiles)
-                    load_tile(tile + 2);
+                f32x16 f;
+                scores_hi(buf, f);
+                scores_lo(buf, f);
+                softmax_pv(tile, buf, f, !next);
             }
+            if (!stage_first)
+                stage();
             __syncthreads();
         }
     }
@@ -624,8 +632,9 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
             if (wave_active)
             {
                 f32x16 f;
-                scores_a(0, f);
-                finish(tile, 0, f);
+                scores_hi(0, f);
+                scores_lo(0, f);
+                softmax_pv(tile, 0, f, tile == tiles - 1);
             }
             __syncthreads();
         }

@@ -30,3 +30,65 @@ def test_plain_reciprocal_without_offset_fails():
         inv = np.float32(1.0) / np.float32(d)
         bad += int(np.count_nonzero((i.astype(np.float32) * inv).astype(np.int64) != i // d))
     assert bad > 0
+
+
+# ---- The fp32 kernel's integer digit slices (awa_attention_x.hip) ----
+# A row value becomes X = trunc(x * 2^(30-e)) (|X| < 2^30) plus the offset
+# 128 (1 + 2^8 + 2^16); four such words are byte-transposed by eight
+# v_perm_b32 (byte i of the result = byte sel_i of the pair (hi, lo), lo the
+# low four bytes) into four int8 slices, the lower three with bit 7 flipped.
+
+
+def _perm(hi, lo, sel):
+    b = [(lo >> (8 * i)) & 255 for i in range(4)] + [(hi >> (8 * i)) & 255 for i in range(4)]
+    return sum(b[(sel >> (8 * i)) & 255] << (8 * i) for i in range(4))
+
+
+def _transpose_digits(x):
+    a = _perm(x[1], x[0], 0x06020400)
+    b = _perm(x[1], x[0], 0x07030501)
+    c = _perm(x[3], x[2], 0x06020400)
+    d = _perm(x[3], x[2], 0x07030501)
+    return [_perm(d, b, 0x07060302), _perm(c, a, 0x07060302) ^ 0x80808080,
+            _perm(d, b, 0x05040100) ^ 0x80808080, _perm(c, a, 0x05040100) ^ 0x80808080]
+
+
+def _int8(word, i):
+    v = (word >> (8 * i)) & 255
+    return v - 256 if v >= 128 else v
+
+
+def test_digit_slices_reconstruct_every_value():
+    """Byte i of slice s is digit s of value i; the digits rebuild X exactly
+    (X = d1 2^24 + d2 2^16 + d3 2^8 + d4), with d1 in [-64, 64] and the
+    balanced lower digits in [-128, 127]."""
+    rng = np.random.default_rng(7)
+    edge = [2**30 - 1, -(2**30) + 1, 0, -1, 1, 0x7F7F7F, -0x808080, 0x808080, -0x7F7F7F, 2**24, -(2**24)]
+    values = edge + [int(v) for v in rng.integers(-(2**30) + 1, 2**30, 40000)]
+    values += [0] * (-len(values) % 4)
+    for q in range(0, len(values), 4):
+        xs = values[q:q + 4]
+        w = _transpose_digits([(x + 0x808080) & 0xFFFFFFFF for x in xs])
+        for i, x in enumerate(xs):
+            d = [_int8(w[s], i) for s in range(4)]
+            assert -64 <= d[0] <= 64 and all(-128 <= v <= 127 for v in d[1:]), (x, d)
+            assert ((d[0] * 256 + d[1]) * 256 + d[2]) * 256 + d[3] == x, (x, d)
+
+
+def test_digit_slices_fail_without_the_flip():
+    """Leaving out the bit-7 flip of the lower slices breaks reconstruction:
+    the check above would catch it."""
+    x = [12345, -6789, 2**29, -(2**29)]
+    w = _transpose_digits([(v + 0x808080) & 0xFFFFFFFF for v in x])
+    w[1] ^= 0x80808080
+    d = [_int8(w[s], 0) for s in range(4)]
+    assert ((d[0] * 256 + d[1]) * 256 + d[2]) * 256 + d[3] != x[0]
+
+
+def test_score_classes_fit_exact_int32_and_fp32():
+    """With |d1| <= 64 and |d2..d4| <= 128 over 128 features, every weight
+    class C_w (w = 2..5, at most four slice products per feature) stays below
+    2^23: exact in the int32 MFMA accumulator and in its fp32 conversion."""
+    bound = {2: 64 * 64, 3: 2 * 64 * 128, 4: 2 * 64 * 128 + 128 * 128, 5: 2 * 64 * 128 + 2 * 128 * 128}
+    for w, per_feature in bound.items():
+        assert per_feature * 128 < 2**23, w
