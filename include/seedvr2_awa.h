@@ -299,10 +299,16 @@ int awa_stack_block_flops(const awa_stack* stack, double* flops);
  * fp32 accumulation and arithmetic (the BF16 blocks, dit_stack.cpp:519,
  * :550). The GEMMs are library GEMMs (hipBLASLt). A block or stack object is
  * used by one thread at a time (it caches GEMM descriptors on first use). The
- * first forward of an object times hipBLASLt's candidate algorithms for each
- * GEMM shape on the caller's operands and stream, waiting for the stream once
- * per shape (not under graph capture, where the heuristic's first is taken);
- * later calls are asynchronous. */
+ * first GEMM of each shape in the process times hipBLASLt's candidate
+ * algorithms on the caller's operands and stream, waiting for the stream once
+ * (not under graph capture, where the heuristic's first is taken for that
+ * call); its choice then holds for every block and stack object of the
+ * process, so equal shapes give equal bits within a process. Timing noise can
+ * still pick a different algorithm in another process, and results then differ
+ * in the last bits (the fp32 and bf16 tolerances hold either way). With the
+ * environment variable SEEDVR2_GEMM_HEURISTIC=1 the heuristic's first
+ * algorithm is taken for every shape, without timing: the same choice in every
+ * process on the same device and library version. */
 typedef struct awa_dit_block_desc {
     int source_t, source_h, source_w;    /* token grid */
     int windows_t, windows_h, windows_w; /* window counts (params 3/4/5) */

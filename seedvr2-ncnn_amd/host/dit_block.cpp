@@ -19,8 +19,10 @@
 #include <hipblaslt/hipblaslt.h>
 
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <new>
 #include <string>
 #include <tuple>
@@ -145,14 +147,32 @@ constexpr size_t kGemmWorkspace = 64u << 20;
 constexpr int kGemmCandidates = 16;
 constexpr int kGemmTimedRuns = 3;
 
+// The algorithm chosen for a GEMM shape, shared by every block object of the
+// process: (device, element size, M, N, K, ldx, ldy) -> algorithm. The first
+// object to meet a shape chooses; every later one, shifted or not, runs the
+// same algorithm, so equal shapes give equal bits within a process.
+std::mutex g_algo_mutex;
+std::map<std::tuple<int, int, int, int, int, long long, long long>, hipblasLtMatmulAlgo_t> g_algos;
+
+// SEEDVR2_GEMM_HEURISTIC=1: take the heuristic's first algorithm instead of
+// timing the candidates, so that the choice (and the output bits) do not
+// depend on timing noise from one process to the next.
+bool heuristic_first()
+{
+    const char* v = std::getenv("SEEDVR2_GEMM_HEURISTIC");
+    return v && v[0] == '1';
+}
+
 // Y[M][N] (row stride ldy) = X[M][K] (row stride ldx) W[N][K]^T, fp32
 // accumulation. Column-major view: Y^T (N x M, ld ldy) = op(A) B with A = W
 // stored K x N (ld K) and transposed, B = X^T (K x M, ld ldx). The
-// descriptors are built once per shape, and the algorithm is chosen then:
-// up to kGemmCandidates of the heuristic's algorithms each run once to warm
-// up and kGemmTimedRuns times under HIP events on the call's own operands
-// (y is rewritten by the call that follows), and the fastest is kept. A
-// stream under graph capture takes the heuristic's first algorithm.
+// descriptors are built once per shape and block object; the algorithm once
+// per shape and process (g_algos): up to kGemmCandidates of the heuristic's
+// algorithms each run once to warm up and kGemmTimedRuns times under HIP
+// events on the call's own operands (y is rewritten by the call that
+// follows), and the fastest is kept. The heuristic's first is taken instead
+// under SEEDVR2_GEMM_HEURISTIC=1 and on a stream under graph capture (not
+// stored, so that a later eager call still chooses for the process).
 int gemm(awa_dit_block* b, const void* x, long long ldx, const void* w, void* y, long long ldy, int M, int N, int K,
          hipStream_t stream)
 {
@@ -188,12 +208,27 @@ int gemm(awa_dit_block* b, const void* x, long long ldx, const void* w, void* y,
         }
         if (pref)
             hipblasLtMatmulPreferenceDestroy(pref);
+        int device = 0;
+        (void)hipGetDevice(&device);
+        const auto algo_key = std::make_tuple(device, b->es, M, N, K, ldx, ldy);
+        bool cached = false;
         if (ok)
+        {
+            std::lock_guard<std::mutex> lock(g_algo_mutex);
+            const auto hit = g_algos.find(algo_key);
+            if (hit != g_algos.end())
+            {
+                g.algo = hit->second;
+                cached = true;
+            }
+        }
+        if (ok && !cached)
         {
             g.algo = results[0].algo;
             hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
             (void)hipStreamIsCapturing(stream, &capture);
-            if (found > 1 && capture == hipStreamCaptureStatusNone)
+            const bool timed = found > 1 && !heuristic_first() && capture == hipStreamCaptureStatusNone;
+            if (timed)
             {
                 hipEvent_t start = nullptr, stop = nullptr;
                 DIT_HIP(hipEventCreate(&start), "hipEventCreate");
@@ -230,6 +265,12 @@ int gemm(awa_dit_block* b, const void* x, long long ldx, const void* w, void* y,
                 (void)hipEventDestroy(start);
                 (void)hipEventDestroy(stop);
                 (void)hipGetLastError();
+            }
+            if (timed || heuristic_first())
+            {
+                // The first choice for a shape stands for the process.
+                std::lock_guard<std::mutex> lock(g_algo_mutex);
+                g.algo = g_algos.emplace(algo_key, g.algo).first->second;
             }
         }
         if (!ok)

@@ -234,3 +234,16 @@ def test_dit_stack_zero_gates_is_exact_at_benchmark_shape(gpu):
     stack.destroy()
     np.testing.assert_array_equal(got_v, O.round_bf16(video))
     np.testing.assert_array_equal(got_t, 2.0 * O.round_bf16(text))
+
+
+@pytest.mark.parametrize("precision", [A.COMPUTE_F32, A.COMPUTE_BF16])
+def test_block_objects_share_gemm_algorithms(gpu, precision):
+    """Two block objects of one shape (the second created after the first
+    chose its GEMM algorithms) run the same algorithms: bit-identical
+    outputs on the same weights and inputs."""
+    print(f"case two block objects precision={precision}", flush=True)
+    g, video, text, emb, wv, wt = case(20260917, False)
+    first = run_block(g, video, text, emb, wv, wt, False, precision)
+    second = run_block(g, video, text, emb, wv, wt, False, precision)
+    for a, b in zip(first, second):
+        assert np.array_equal(a, b)
