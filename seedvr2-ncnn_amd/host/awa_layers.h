@@ -208,11 +208,12 @@ private:
 
 // Runs a loaded net the way ncnn::Extractor does: input() binds blobs by
 // name (the Input layers' tops), extract() runs the layers the requested blob
-// depends on, in file order, and returns it. Runs the created layers and
+// depends on, in file order, and returns it. Runs the created layers,
 // ncnn's Reshape (params 0 = w, 1 = h, 11 = d, 2 = c; -1 inferred, 0 keeps
 // the input's extent; padded inputs are first copied dense, as ncnn's Reshape
-// does with a flattened copy); a needed layer of any other type fails the
-// extraction with -1. Enqueued on the net option's stream.
+// does with a flattened copy) and Split (every top shares the bottom); a
+// needed layer of any other type fails the extraction with -1. Enqueued on
+// the net option's stream.
 class Extractor
 {
 public:
