@@ -320,6 +320,12 @@ typedef struct awa_dit_block_desc {
     int last_layer;
     int precision;        /* AWA_COMPUTE_F32 or AWA_COMPUTE_BF16 */
     float norm_eps;       /* 1e-5 */
+    /* No counterpart in the reference. bf16 blocks only; 0 (default) projects
+     * QKV with hipBLASLt and applies the q/k RMSNorm and RoPE in the attention
+     * gather. 1: the library's own MFMA GEMM projects QKV and applies the
+     * q/k RMSNorm and the RoPE rotation in its epilogue (each rounded to bf16
+     * where the reference stores it); the attention then reads rotated Q/K. */
+    int fused_qkv;
 } awa_dit_block_desc;
 
 /* Device weights of one branch (video or text). GEMM weights are row-major

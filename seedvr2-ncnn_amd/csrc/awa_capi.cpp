@@ -724,7 +724,7 @@ void set_error(const std::string& message)
 
 int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv, const awa_qk_norm* norm,
                   const awa_blob* video_out, const awa_blob* text_out, int compute, hipStream_t stream,
-                  hipEvent_t after_attention, const Scratch* scratch)
+                  hipEvent_t after_attention, const Scratch* scratch, bool pre_rotated)
 {
     int rc = check_plan_uploaded(plan);
     if (rc != AWA_OK)
@@ -733,6 +733,8 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
         return fail(AWA_ERR_INVALID, "null blob");
     if (!valid_compute(compute))
         return fail(AWA_ERR_INVALID, "unknown compute mode");
+    if (pre_rotated && (compute != AWA_COMPUTE_BF16 || norm))
+        return fail(AWA_ERR_INVALID, "pre-rotated Q/K need the bf16 kernel and no fused norm");
     trace_blob("forward.video.in", video_qkv);
     trace_blob("forward.text.in", text_qkv);
     trace_blob("forward.video.out", video_out);
@@ -806,6 +808,7 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
     p.video_out = sink;
     p.text_partials = partials;
     p.text_partial_elemsize = static_cast<int>(text_out->elemsize);
+    p.pre_rotated = pre_rotated;
     if (norm)
     {
         p.qk_norm = true;
