@@ -66,8 +66,9 @@ __global__ __launch_bounds__(kThreads, 2) void qkv_rope_gemm_kernel(const QkvRop
     const int m0 = (slot % blocks_m) * kTokens;
     const int f0 = head_block * kFeatures;
 
-    // Slice staging: thread t moves 16 bytes (8 k) of rows t / 8 + 32 j of
-    // the W and X slices; 8 consecutive threads cover one row's 128 bytes.
+    // Slice staging: thread t moves 16 bytes (8 k) of rows t / 8 + 32 i
+    // (i < 4) of the W and X slices; 8 consecutive threads cover one row's
+    // 128 bytes.
     const int lr = tid >> 3;
     const int lk = 8 * (tid & 7);
     // Two register stages, each a slice of W and X rows on its way to LDS
