@@ -46,7 +46,15 @@ def qkv_inputs(g: O.Geometry, heads: int, head_dim: int, seed: int):
 
 
 def rel_err(got: np.ndarray, ref: np.ndarray) -> float:
-    return float(np.max(np.abs(got.astype(np.float64) - ref)) / max(np.max(np.abs(ref)), 1e-30))
+    """max|got - ref| / max|ref|, the bf16 gate. Also prints the Frobenius
+    relative error and per-element statistics of the same comparison."""
+    d = np.abs(got.astype(np.float64) - np.asarray(ref, np.float64))
+    r = np.asarray(ref, np.float64)
+    gate = float(np.max(d) / max(np.max(np.abs(r)), 1e-30))
+    fro = float(np.linalg.norm(d) / max(np.linalg.norm(r), 1e-30))
+    print(f"  bf16 check: max rel {gate:.3g}, Frobenius rel {fro:.3g}, mean |d| {np.mean(d):.3g}, "
+          f"p99.9 |d| {np.quantile(d, 0.999):.3g}, max |d| {np.max(d):.3g} over {d.size} elements", flush=True)
+    return gate
 
 
 def abs_err(got: np.ndarray, ref: np.ndarray) -> float:

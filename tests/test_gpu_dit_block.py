@@ -77,7 +77,11 @@ def run_block(g, video, text, emb, wv, wt, last_layer, precision, fused_qkv=Fals
 
 
 def rel(a, b):
-    return float(np.max(np.abs(a.astype(np.float64) - b)) / np.max(np.abs(b)))
+    """max|a - b| / max|b| (the gate), with the Frobenius relative error printed beside it."""
+    d = np.abs(a.astype(np.float64) - b)
+    fro = float(np.linalg.norm(d) / np.linalg.norm(np.asarray(b, np.float64)))
+    print(f"  Frobenius rel {fro:.3g}, mean |d| {np.mean(d):.3g}", flush=True)
+    return float(np.max(d) / np.max(np.abs(b)))
 
 
 @pytest.mark.parametrize("last_layer", [False, True])
