@@ -268,6 +268,26 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
 
     auto store_k_from = [&](int tile, int buf, const uint32_t* src) {
         unsigned char* const kb = k_lds + buf * kKBytes;
+        // The (cos, sin) of every pair of this thread's K rows are read before
+        // any is used, so that their LDS latency is paid once per tile rather
+        // than once per row and pair (in the bf16 kernels a scheduling
+        // barrier keeps the compiler from interleaving them back).
+        float2 cs[FUSED ? kKRows : 1][4];
+        if constexpr (FUSED)
+        {
+            uint32_t code[kKRows];
+#pragma unroll
+            for (int j = 0; j < kKRows; j++)
+                code[j] = row_code[tile * KT + kr0 + kRowsPerPass * j];
+#pragma unroll
+            for (int j = 0; j < kKRows; j++)
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    cs[j][q] = *reinterpret_cast<const float2*>(rope_lds + ((code[j] >> rope_shift[q]) & 255u) * kRopeRow +
+                                                                rope_col[q]);
+            if constexpr (BF16)
+                __builtin_amdgcn_sched_barrier(0);
+        }
 #pragma unroll
         for (int j = 0; j < kKRows; j++)
         {
@@ -295,16 +315,13 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
                     for (int e = 0; e < 8; e++)
                         kv[e] = (kv[e] * coef) * gv[e];
                 }
-                const uint32_t code = row_code[tile * KT + row];
 #pragma unroll
                 for (int q = 0; q < 4; q++)
                 {
-                    const uint32_t coord = (code >> rope_shift[q]) & 255u;
-                    const float2 t = *reinterpret_cast<const float2*>(rope_lds + coord * kRopeRow + rope_col[q]);
                     if constexpr (BF16)
-                        rope_pair_fma(kv[2 * q], kv[2 * q + 1], t.x, t.y);
+                        rope_pair_fma(kv[2 * q], kv[2 * q + 1], cs[j][q].x, cs[j][q].y);
                     else
-                        rope_pair_cs(kv[2 * q], kv[2 * q + 1], t.x, t.y);
+                        rope_pair_cs(kv[2 * q], kv[2 * q + 1], cs[j][q].x, cs[j][q].y);
                 }
             }
             if constexpr (BF16)
@@ -520,20 +537,32 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
                 c0 = negm;
             const uint16_t* ks =
                 reinterpret_cast<const uint16_t*>(k_lds + buf * kKBytes) + krow * kKPitch + 8 * half;
+            // The K operand reads run kAhead feature steps ahead of the MFMAs
+            // that use them. The scheduling barriers pin that order: left to
+            // itself the compiler sinks each read next to its MFMA, behind a
+            // wait for that read alone, and every MFMA then waits a full LDS
+            // latency. (The narrow kernels on fp32 input keep one read ahead:
+            // their register stages leave no room for more.)
+            constexpr int kAhead = WIDE || sizeof(TIn) == 2 ? 3 : 1;
             bf16x8 ka[kBlocks][8];
 #pragma unroll
-            for (int c = 0; c < 8; c++)
+            for (int c = 0; c < kAhead; c++)
 #pragma unroll
                 for (int b = 0; b < kBlocks; b++)
                     ka[b][c] = *reinterpret_cast<const bf16x8*>(ks + b * 32 * kKPitch + 16 * c);
 #pragma unroll
-            for (int b = 0; b < kBlocks; b++)
-                s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[b][0], qb[0], c0, 0, 0, 0);
+            for (int c = 0; c < 8; c++)
+            {
+                if (c + kAhead < 8)
 #pragma unroll
-            for (int c = 1; c < 8; c++)
+                    for (int b = 0; b < kBlocks; b++)
+                        ka[b][c + kAhead] = *reinterpret_cast<const bf16x8*>(ks + b * 32 * kKPitch + 16 * (c + kAhead));
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int b = 0; b < kBlocks; b++)
-                    s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[b][c], qb[c], s[b], 0, 0, 0);
+                    s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[b][c], qb[c], c == 0 ? c0 : s[b], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
         else
         {
