@@ -177,21 +177,24 @@ def host_cpu() -> dict:
     return {"cpu_model": model, "nproc": os.cpu_count(), "usable_cpus": len(os.sched_getaffinity(0))}
 
 
-# The BASELINE workloads, each run as a stack of attention layers with even
-# layers unshifted and odd layers shifted: (latent t, h, w), window counts,
-# arithmetic, the layers the config is quoted on.
+# The workloads the metric is quoted on: the 1-frame 256x256 fp32 image
+# layer, a 5-frame bf16 clip (shifted), the 33-frame 256x256 mixed step, a
+# 33-frame 512x512 bf16 clip and a 121-frame 256x256 bf16 clip. Each runs as
+# a stack of attention layers with even layers unshifted and odd layers
+# shifted: (latent t, h, w), window counts, arithmetic, the layers it is
+# quoted on.
 CONFIGS = {
-    "cfg1_fp32_image_1x16x16": ((1, 16, 16), (1, 8, 8), "fp32", ("unshifted",)),
-    "cfg2_bf16_shifted_2x16x16": ((2, 16, 16), (1, 8, 8), "bf16", ("shifted",)),
-    "cfg3_mixed_9x16x16": ((9, 16, 16), (3, 8, 8), "mixed", ("unshifted", "shifted")),
-    "cfg4_bf16_9x32x32": ((9, 32, 32), (3, 8, 8), "bf16", ("unshifted", "shifted")),
-    "cfg5_bf16_31x16x16": ((31, 16, 16), (8, 8, 8), "bf16", ("unshifted", "shifted")),
+    "fp32_image_1x16x16": ((1, 16, 16), (1, 8, 8), "fp32", ("unshifted",)),
+    "bf16_shifted_clip_2x16x16": ((2, 16, 16), (1, 8, 8), "bf16", ("shifted",)),
+    "mixed_step_9x16x16": ((9, 16, 16), (3, 8, 8), "mixed", ("unshifted", "shifted")),
+    "bf16_clip_512_9x32x32": ((9, 32, 32), (3, 8, 8), "bf16", ("unshifted", "shifted")),
+    "bf16_clip_121f_31x16x16": ((31, 16, 16), (8, 8, 8), "bf16", ("unshifted", "shifted")),
 }
 MALL_BYTES = 256 * 1024 * 1024
 
 
 def config_measurements(A, stream, steps: int = 10, profile_steps: int = 5) -> dict:
-    """Every BASELINE config in two regimes. HBM-cold: every layer reads its
+    """Every workload above in two regimes. HBM-cold: every layer reads its
     own inputs and the stack's inputs and outputs total at least 1 GiB (four
     times the 256 MB Infinity Cache), so no layer finds its data cached.
     MALL-warm: every layer of the stack reads the same inputs, which stay in
@@ -279,8 +282,8 @@ def config_measurements(A, stream, steps: int = 10, profile_steps: int = 5) -> d
     return out
 
 
-def cpu_baseline_cfg1() -> dict:
-    """The reference's CPU semantics on BASELINE's CPU-runnable case, the fp32
+def cpu_baseline_image() -> dict:
+    """The reference's CPU semantics on its CPU-runnable case, the fp32
     image layer (1x16x16, windows 1x8x8, 64 text tokens, 20 heads): the
     oracle's single-threaded restatement of the CPU forward, whole layer."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -438,7 +441,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dit-step", action="store_true", help="skip the full 32-block DiT step measurement")
     ap.add_argument("--no-configs", action="store_true",
-                    help="skip the per-config table (every BASELINE config, HBM-cold and MALL-warm)")
+                    help="skip the per-workload table (every quoted workload, HBM-cold and MALL-warm)")
     ap.add_argument("--dit-steps", type=int, default=5)
     ap.add_argument("--cpu-sample-layers", type=int, default=2, choices=(1, 2))
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "awa_attention_hbm_traffic.json"),
@@ -605,7 +608,7 @@ def main() -> int:
         result["fused_qkv_block"] = fused_qkv_block(A, stream)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_sample_layers)
-        result["cpu_baseline_cfg1"] = cpu_baseline_cfg1()
+        result["cpu_baseline_fp32_image"] = cpu_baseline_image()
     print(json.dumps(result), flush=True)
     stack.destroy()
     stream.destroy()
