@@ -36,16 +36,18 @@ extern "C" {
 #define AWA_ERR_ALLOC (-100)
 
 /* Arithmetic of the attention contractions. AWA_COMPUTE_F32 (the reference's
- * FP32 blocks) takes fp32 Q, K, V and computes each score q.k nearly exactly
- * before one fp32 rounding, as the reference's Kahan-sum shaders do: Q and K
- * rows are split into four signed 7-bit digit slices under a per-row power of
- * two and multiplied on int8 matrix cores with exact int32 sums; P V uses P as
- * two bf16 pieces and V as three (the fp32 value) on bf16 matrix cores with
- * fp32 accumulation. AWA_COMPUTE_BF16 rounds Q, K, V and P to bf16 and
- * accumulates in fp32 on bf16 MFMA (BF16 blocks). AWA_COMPUTE_F32_MFMA runs
- * QK^T and PV on fp32 MFMA with plain fp32 accumulation (slower, and less
- * accurate when scores are large or cancel; kept for comparison). Softmax
- * statistics are fp32 in all three. */
+ * AWA arithmetic, which is fp32 in every block: src/awa/awa_layers.cpp:202-212)
+ * takes fp32 or bf16 Q, K, V. It computes each score q.k as a correctly
+ * rounded fp32 dot product, the accuracy the reference's Kahan-sum shaders
+ * aim for. Q and K rows are written as four balanced base-256 digit slices
+ * under a per-row power of two and multiplied on int8 matrix cores with exact
+ * int32 sums. P V uses P and V as three bf16 pieces each (all 24 bits of the
+ * fp32 values) on bf16 matrix cores with fp32 accumulation. AWA_COMPUTE_BF16
+ * rounds Q, K, V and P to bf16 and accumulates in fp32 on bf16 MFMA; this is
+ * the bf16-MFMA arithmetic of the BF16 blocks. AWA_COMPUTE_F32_MFMA runs QK^T
+ * and PV on fp32 MFMA with plain fp32 accumulation. It is slower, and less
+ * accurate when scores are large or cancel; it is kept for comparison.
+ * Softmax statistics are fp32 in all three. */
 #define AWA_COMPUTE_F32 0
 #define AWA_COMPUTE_BF16 1
 #define AWA_COMPUTE_F32_MFMA 2
