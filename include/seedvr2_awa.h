@@ -36,7 +36,7 @@ extern "C" {
 #define AWA_ERR_ALLOC (-100)
 
 /* Arithmetic of the attention contractions. AWA_COMPUTE_F32 (the reference's
- * AWA arithmetic, which is fp32 in every block: src/awa/awa_layers.cpp:202-212)
+ * AWA arithmetic, which is fp32 in every block: src/awa/awa_layers.cpp:203-213)
  * takes fp32 or bf16 Q, K, V. It computes each score q.k as a correctly
  * rounded fp32 dot product, the accuracy the reference's Kahan-sum shaders
  * aim for. Q and K rows are written as four balanced base-256 digit slices
