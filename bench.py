@@ -383,55 +383,6 @@ def dit_step(A, stream, steps: int, warmup: int = 2) -> dict:
     }
 
 
-def fused_qkv_block(A, stream, iters: int = 20) -> dict:
-    """One bf16 DiT block at the same workload (unshifted and shifted
-    windows), its QKV projection on hipBLASLt with the q/k RMSNorm and RoPE
-    in the attention gather (the default) against the library's own MFMA GEMM
-    with the RMSNorm and RoPE in its epilogue (fused_qkv). Random-init bf16
-    weights N(0, 0.02), inputs N(0, 1); us per block forward (HIP events,
-    mean over `iters` after warm-up)."""
-    t, h, w = GRID
-    N = t * h * w
-    hidden, hd, mh = HEADS * HEAD_DIM, HEADS * HEAD_DIM, MLP_HIDDEN
-    keep = []
-    seed = [9500]
-
-    def buf(count, es, stddev=0.02):
-        b = A.DeviceBuffer(count * es)
-        b.fill_normal(count, es, seed[0], stream, stddev)
-        seed[0] += 1
-        keep.append(b)
-        return b.ptr
-
-    def branch():
-        pair = buf(2 * mh * hidden, 2)
-        return A.AwaDitBranchWeights(buf(3 * hd * hidden, 2), buf(hidden * hd, 2), buf(hidden, 4), pair,
-                                     pair + mh * hidden * 2, buf(hidden * mh, 2), buf(HEAD_DIM, 4),
-                                     buf(HEAD_DIM, 4), buf(6 * hidden, 4))
-
-    wv, wt = branch(), branch()
-    video, text, emb = buf(N * hidden, 2, 1.0), buf(TEXT * hidden, 2, 1.0), buf(6 * hidden, 2, 1.0)
-    vout, tout = buf(N * hidden, 2, 1.0), buf(TEXT * hidden, 2, 1.0)
-    out = {}
-    for shifted in (False, True):
-        for fused in (False, True):
-            blk = A.DitBlock(t, h, w, *WINDOWS, TEXT, shifted, HEADS, HEAD_DIM, hidden, mh, False, A.COMPUTE_BF16,
-                             1e-5, fused)
-            for _ in range(3):
-                blk.forward(wv, wt, video, text, emb, vout, tout, stream)
-            e0, e1 = A.Event(), A.Event()
-            e0.record(stream)
-            for _ in range(iters):
-                blk.forward(wv, wt, video, text, emb, vout, tout, stream)
-            e1.record(stream)
-            stream.synchronize()
-            key = ("shifted" if shifted else "unshifted") + ("_fused_qkv" if fused else "_default")
-            out[key + "_us"] = round(e0.elapsed_ms(e1) / iters * 1e3, 1)
-            blk.destroy()
-    out["data"] = "bf16 block, hidden 2560, SwiGLU 6912, random-init weights N(0, 0.02), inputs N(0, 1)"
-    return out
-
-
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -605,7 +556,6 @@ def main() -> int:
         result["configs"] = config_measurements(A, stream)
     if not args.no_dit_step:
         result["dit_step"] = dit_step(A, stream, args.dit_steps)
-        result["fused_qkv_block"] = fused_qkv_block(A, stream)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_sample_layers)
         result["cpu_baseline_fp32_image"] = cpu_baseline_image()

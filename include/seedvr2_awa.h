@@ -19,7 +19,11 @@
  *    and is asynchronous; the caller synchronises (awa_stream_synchronize
  *    replaces the reference's submit_and_wait_profiled).
  *  - Plans are immutable after awa_plan_upload except for their device
- *    workspace: calls that use one plan on several streams at once race on it.
+ *    workspace (work list, text rows). A forward holds the plan's lock from
+ *    its workspace check until its kernels are enqueued, so calls from several
+ *    threads never launch on a freed work list; but a call with another head
+ *    count replaces the workspace while kernels of an earlier call on another
+ *    stream may still read it. Use one plan per stream.
  */
 #ifndef SEEDVR2_AWA_H
 #define SEEDVR2_AWA_H
@@ -322,12 +326,6 @@ typedef struct awa_dit_block_desc {
     int last_layer;
     int precision;        /* AWA_COMPUTE_F32 or AWA_COMPUTE_BF16 */
     float norm_eps;       /* 1e-5 */
-    /* No counterpart in the reference. bf16 blocks only; 0 (default) projects
-     * QKV with hipBLASLt and applies the q/k RMSNorm and RoPE in the attention
-     * gather. 1: the library's own MFMA GEMM projects QKV and applies the
-     * q/k RMSNorm and the RoPE rotation in its epilogue (each rounded to bf16
-     * where the reference stores it); the attention then reads rotated Q/K. */
-    int fused_qkv;
 } awa_dit_block_desc;
 
 /* Device weights of one branch (video or text). GEMM weights are row-major

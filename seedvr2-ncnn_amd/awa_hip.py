@@ -86,8 +86,7 @@ class AwaDitBlockDesc(ctypes.Structure):
     """awa_dit_block_desc."""
     _fields_ = [(name, ctypes.c_int) for name in (
         "source_t", "source_h", "source_w", "windows_t", "windows_h", "windows_w", "text_tokens", "shifted",
-        "heads", "head_dim", "hidden", "mlp_hidden", "last_layer", "precision")] + [("norm_eps", ctypes.c_float),
-                                                                                     ("fused_qkv", ctypes.c_int)]
+        "heads", "head_dim", "hidden", "mlp_hidden", "last_layer", "precision")] + [("norm_eps", ctypes.c_float)]
 
 
 class AwaDitStackDesc(ctypes.Structure):
@@ -428,9 +427,9 @@ class DitBlock:
 
     def __init__(self, t: int, h: int, w: int, nt: int, nh: int, nw: int, text_tokens: int, shifted: bool,
                  heads: int, head_dim: int, hidden: int, mlp_hidden: int, last_layer: bool, precision: int,
-                 norm_eps: float = 1e-5, fused_qkv: bool = False):
+                 norm_eps: float = 1e-5):
         self.desc = AwaDitBlockDesc(t, h, w, nt, nh, nw, text_tokens, int(shifted), heads, head_dim, hidden,
-                                    mlp_hidden, int(last_layer), precision, norm_eps, int(fused_qkv))
+                                    mlp_hidden, int(last_layer), precision, norm_eps)
         p = ctypes.c_void_p()
         check(lib().awa_dit_block_create(ctypes.byref(self.desc), ctypes.byref(p)), "awa_dit_block_create")
         self.handle = p.value

@@ -191,12 +191,8 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
             const TIn* const k_ptr = source_ptr(r, 1);
             row_k[i] = reinterpret_cast<const unsigned char*>(k_ptr) - load_base;
             row_v[i] = reinterpret_cast<const unsigned char*>(k_ptr + (r.text ? t_qkv : v_qkv)) - load_base;
-            // Pre-rotated Q/K: every coordinate names the identity row, whose
-            // (cos, sin) = (1, 0) leaves each pair as it is.
-            row_code[i] = p.pre_rotated ? static_cast<uint32_t>(p.rope_coords) * 0x01010101u
-                                        : static_cast<uint32_t>(r.ct) | (static_cast<uint32_t>(r.ch) << 8) |
-                                              (static_cast<uint32_t>(r.cw) << 16) |
-                                              (static_cast<uint32_t>(p.rope_coords) << 24);
+            row_code[i] = static_cast<uint32_t>(r.ct) | (static_cast<uint32_t>(r.ch) << 8) |
+                          (static_cast<uint32_t>(r.cw) << 16) | (static_cast<uint32_t>(p.rope_coords) << 24);
         }
         else
         {

@@ -285,10 +285,11 @@ std::vector<awa::WorkItem> build_work(const awa_plan& plan, int heads, int rows_
 }
 
 // Ensures the plan's work list for `heads` and a text-partials buffer of at
-// least `partial_bytes` exist on the device.
-int ensure_workspace(const awa_plan& plan, int heads, size_t partial_bytes)
+// least `partial_bytes` exist on the device. The caller holds plan.mutex, and
+// keeps holding it until the kernels that read the work list are enqueued, so
+// that no other call replaces the list in between.
+int ensure_workspace_locked(const awa_plan& plan, int heads, size_t partial_bytes)
 {
-    std::lock_guard<std::mutex> lock(plan.mutex);
     if (plan.work_heads != heads || !plan.work)
     {
         for (const bool wide : {false, true})
@@ -681,7 +682,8 @@ int upload_plan(awa_plan* plan, void* stream)
     const int rc = awa_plan_upload_tables(plan, stream);
     if (rc != AWA_OK || plan->heads_hint <= 0)
         return rc;
-    return ensure_workspace(*plan, plan->heads_hint, 0);
+    std::lock_guard<std::mutex> lock(plan->mutex);
+    return ensure_workspace_locked(*plan, plan->heads_hint, 0);
 }
 
 } // namespace
@@ -724,7 +726,7 @@ void set_error(const std::string& message)
 
 int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv, const awa_qk_norm* norm,
                   const awa_blob* video_out, const awa_blob* text_out, int compute, hipStream_t stream,
-                  hipEvent_t after_attention, const Scratch* scratch, bool pre_rotated)
+                  hipEvent_t after_attention, const Scratch* scratch)
 {
     int rc = check_plan_uploaded(plan);
     if (rc != AWA_OK)
@@ -733,8 +735,6 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
         return fail(AWA_ERR_INVALID, "null blob");
     if (!valid_compute(compute))
         return fail(AWA_ERR_INVALID, "unknown compute mode");
-    if (pre_rotated && (compute != AWA_COMPUTE_BF16 || norm))
-        return fail(AWA_ERR_INVALID, "pre-rotated Q/K need the bf16 kernel and no fused norm");
     trace_blob("forward.video.in", video_qkv);
     trace_blob("forward.text.in", text_qkv);
     trace_blob("forward.video.out", video_out);
@@ -775,6 +775,9 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
     }
 
     void* partials = nullptr;
+    // Held until both kernels are enqueued: they read the plan's work list
+    // and text workspace, which a call with another head count replaces.
+    std::lock_guard<std::mutex> lock(plan->mutex);
     if (scratch)
     {
         // No allocation: the text rows in the caller's buffer, the work list
@@ -785,7 +788,6 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
             return fail(AWA_ERR_INVALID, "text rows of this layer need " + std::to_string(need) +
                                              " bytes, more than the no-alloc scratch buffer's " +
                                              std::to_string(scratch->bytes));
-        std::lock_guard<std::mutex> lock(plan->mutex);
         if (plan->work_heads != vl.heads || !plan->work)
             return fail(AWA_ERR_INVALID, "plan has no work list for " + std::to_string(vl.heads) +
                                              " heads: create it with awa_plan_desc.heads set, or run awa_forward once");
@@ -795,7 +797,7 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
     {
         const size_t partial_bytes = plan->windows.size() * static_cast<size_t>(plan->text_tokens) * vl.heads *
                                      vl.head_dim * sizeof(float);
-        if ((rc = ensure_workspace(*plan, vl.heads, partial_bytes)) != AWA_OK)
+        if ((rc = ensure_workspace_locked(*plan, vl.heads, partial_bytes)) != AWA_OK)
             return rc;
         partials = plan->text_partials;
     }
@@ -808,7 +810,6 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
     p.video_out = sink;
     p.text_partials = partials;
     p.text_partial_elemsize = static_cast<int>(text_out->elemsize);
-    p.pre_rotated = pre_rotated;
     if (norm)
     {
         p.qk_norm = true;
@@ -941,7 +942,8 @@ int awa_window_attention(const awa_plan* plan, const awa_blob* input, const awa_
     const int align_elems = 16 / input->elemsize;
     if (!aligned16(input->data) || input->cstep % align_elems || !aligned16(output->data) || output->cstep % 4)
         return fail(AWA_ERR_INVALID, "packed blobs must be 16-byte aligned with 16-byte aligned strides");
-    if ((rc = ensure_workspace(*plan, heads, 0)) != AWA_OK)
+    std::lock_guard<std::mutex> lock(plan->mutex); // until the launch reads the work list
+    if ((rc = ensure_workspace_locked(*plan, heads, 0)) != AWA_OK)
         return rc;
     awa::AttentionLaunch p{};
     p.fused = false;

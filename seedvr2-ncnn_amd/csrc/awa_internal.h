@@ -26,11 +26,9 @@ struct Scratch
 // per-kernel timing). scratch null: the text rows go to the plan's
 // workspace (allocated on first use, with the work list). scratch set: they
 // go there, and nothing is allocated; the plan must already hold the work
-// list for the head count. pre_rotated (bf16 MFMA only, no norm): Q and K
-// already carry the q/k RMSNorm and the RoPE rotation (the DiT block's fused
-// QKV projection); the gather then leaves them unrotated.
+// list for the head count.
 int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv, const awa_qk_norm* norm,
                   const awa_blob* video_out, const awa_blob* text_out, int compute, hipStream_t stream,
-                  hipEvent_t after_attention, const Scratch* scratch = nullptr, bool pre_rotated = false);
+                  hipEvent_t after_attention, const Scratch* scratch = nullptr);
 
 } // namespace awa

@@ -53,9 +53,6 @@ struct AttentionLaunch
     VideoSink video_out;
     void* text_partials;  // [nwin][T_x][H][d], fp32 or bf16 (text_partial_elemsize)
     int text_partial_elemsize;
-    // fused mode: Q and K arrive rotated (every row takes the RoPE table's
-    // identity row)
-    bool pre_rotated;
     // fused q/k RMSNorm over head_dim: gammas q video, k video, q text, k text
     bool qk_norm;
     const float* norm_gamma[4];

@@ -61,31 +61,6 @@ struct SwiGlu
     int rows, width;
 };
 
-// y = x w^T (bf16, fp32 accumulation) for m rows of x [m][k] and the
-// 3 * heads heads of 128 features of w [3 * heads * 128][k]; for q and k
-// heads the DitRMSNorm over the head times gamma, then the MMRoPE rotation of
-// features 0..125 with the token's coordinates (token_code[t] = ct | ch << 8
-// | cw << 16; text rows use their index on all three axes), each step rounded
-// to bf16. k a multiple of 128, ldx and ldw multiples of 8, ldy of 4.
-struct QkvRopeGemm
-{
-    const uint16_t* x;
-    long long ldx;
-    const uint16_t* w;
-    long long ldw;
-    uint16_t* y;
-    long long ldy;
-    int m, k, heads;
-    const float* gamma_q;
-    const float* gamma_k;
-    float eps;
-    const float* rope_cs; // [coords][21][cos, sin]
-    const uint32_t* token_code;
-    bool text;
-};
-
-hipError_t launch_qkv_rope_gemm(const QkvRopeGemm& p, hipStream_t stream);
-
 hipError_t launch_rmsnorm_modulate(const RowNormModulate& p, hipStream_t stream);
 hipError_t launch_gate_residual(const GateResidual& p, hipStream_t stream);
 hipError_t launch_swiglu(const SwiGlu& p, hipStream_t stream);

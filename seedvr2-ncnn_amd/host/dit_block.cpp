@@ -55,9 +55,6 @@ struct awa_dit_block
     // the branch's Ada vectors [6][hidden] fp32.
     void* ws[2][7] = {};
     float* ada[2] = {nullptr, nullptr};
-    // fused_qkv: RoPE coordinates of each video token in its window (ct | ch
-    // << 8 | cw << 16), for the QKV projection's epilogue.
-    uint32_t* token_code = nullptr;
 };
 
 namespace
@@ -96,9 +93,6 @@ int fail_hip(hipError_t e, const char* what)
 
 void release(awa_dit_block* b)
 {
-    if (b->token_code)
-        (void)hipFree(b->token_code);
-    b->token_code = nullptr;
     for (auto& branch : b->ws)
         for (void*& p : branch)
         {
@@ -329,8 +323,6 @@ int awa_dit_block_create(const awa_dit_block_desc* desc, awa_dit_block** out)
         desc->hidden % 8 || desc->mlp_hidden % 8 || desc->hidden > 8192)
         return fail(AWA_ERR_INVALID,
                     "invalid DiT block description (head_dim must be 128, widths multiples of 8, hidden <= 8192)");
-    if (desc->fused_qkv && (desc->precision != AWA_COMPUTE_BF16 || desc->hidden % 64))
-        return fail(AWA_ERR_INVALID, "fused_qkv needs a bf16 block and hidden a multiple of 64");
     awa_dit_block* b = new (std::nothrow) awa_dit_block;
     if (!b)
         return fail(AWA_ERR_ALLOC, "block allocation failed");
@@ -362,26 +354,6 @@ int awa_dit_block_create(const awa_dit_block_desc* desc, awa_dit_block** out)
     }
     b->tokens[0] = desc->source_t * desc->source_h * desc->source_w;
     b->tokens[1] = desc->text_tokens;
-    if (desc->fused_qkv)
-    {
-        // Each video token's window-local RoPE coordinates: those of its
-        // packed row (src/awa/awa_layers.cpp:885-899).
-        std::vector<uint32_t> code(b->tokens[0]);
-        for (int v = 0; v < b->tokens[0]; v++)
-        {
-            const awa::RowInfo& r = b->plan->rows[b->plan->video_positions[v]];
-            code[v] = static_cast<uint32_t>(r.ct) | (static_cast<uint32_t>(r.ch) << 8) |
-                      (static_cast<uint32_t>(r.cw) << 16);
-        }
-        if (hipMalloc(&b->token_code, code.size() * sizeof(uint32_t)) != hipSuccess ||
-            hipMemcpy(b->token_code, code.data(), code.size() * sizeof(uint32_t), hipMemcpyHostToDevice) !=
-                hipSuccess)
-        {
-            release(b);
-            delete b;
-            return fail(AWA_ERR_ALLOC, "RoPE coordinate table allocation failed");
-        }
-    }
     const long long hd = static_cast<long long>(desc->heads) * desc->head_dim;
     for (int br = 0; br < 2; br++)
     {
@@ -450,41 +422,18 @@ int awa_dit_block_forward(awa_dit_block* b, const awa_dit_branch_weights* video_
         nm.shift = modulate ? b->ada[br] + 0 * hidden : nullptr;
         nm.scale = modulate ? b->ada[br] + 1 * hidden : nullptr;
         DIT_HIP(awa::launch_rmsnorm_modulate(nm, stream), "rmsnorm_modulate launch");
-        if (d.fused_qkv)
-        {
-            // QKV with the q/k RMSNorm and the RoPE rotation in the GEMM's epilogue.
-            awa::QkvRopeGemm g{};
-            g.x = static_cast<const uint16_t*>(b->ws[br][kNorm]);
-            g.ldx = hidden;
-            g.w = static_cast<const uint16_t*>(W[br]->qkv);
-            g.ldw = hidden;
-            g.y = static_cast<uint16_t*>(b->ws[br][kQkv]);
-            g.ldy = 3LL * hd;
-            g.m = M;
-            g.k = hidden;
-            g.heads = d.heads;
-            g.gamma_q = W[br]->norm_q;
-            g.gamma_k = W[br]->norm_k;
-            g.eps = d.norm_eps;
-            g.rope_cs = b->plan->dev.rope_cs;
-            g.token_code = b->token_code;
-            g.text = br == 1;
-            DIT_HIP(awa::launch_qkv_rope_gemm(g, stream), "qkv_rope_gemm launch");
-        }
-        else if ((rc = gemm(b, b->ws[br][kNorm], hidden, W[br]->qkv, b->ws[br][kQkv], 3LL * hd, M, 3 * hd, hidden,
-                            stream)) != AWA_OK)
+        if ((rc = gemm(b, b->ws[br][kNorm], hidden, W[br]->qkv, b->ws[br][kQkv], 3LL * hd, M, 3 * hd, hidden,
+                       stream)) != AWA_OK)
             return rc;
     }
-    // AWA with the q/k RMSNorm fused into its gather, or on Q/K the fused
-    // projection already normalised and rotated.
+    // AWA with the q/k RMSNorm fused into its gather.
     {
         const awa_blob vq = dense3(b->ws[0][kQkv], d.head_dim, 3 * d.heads, b->tokens[0], es);
         const awa_blob tq = dense3(b->ws[1][kQkv], d.head_dim, 3 * d.heads, b->tokens[1], es);
         const awa_blob vo = dense3(b->ws[0][kAtt], d.head_dim, d.heads, b->tokens[0], es);
         const awa_blob to = dense3(b->ws[1][kAtt], d.head_dim, d.heads, b->tokens[1], es);
         awa_qk_norm norm{video_w->norm_q, video_w->norm_k, text_w->norm_q, text_w->norm_k, d.norm_eps};
-        if ((rc = awa::forward_fused(b->plan, &vq, &tq, d.fused_qkv ? nullptr : &norm, &vo, &to, d.precision, stream,
-                                     nullptr, nullptr, d.fused_qkv != 0)) != AWA_OK)
+        if ((rc = awa::forward_fused(b->plan, &vq, &tq, &norm, &vo, &to, d.precision, stream, nullptr)) != AWA_OK)
             return rc;
     }
     for (int br = 0; br < 2; br++)

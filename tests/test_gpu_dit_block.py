@@ -62,10 +62,9 @@ def download_act(buf, shape, es):
     return buf.download((n,), np.float32).reshape(shape)
 
 
-def run_block(g, video, text, emb, wv, wt, last_layer, precision, fused_qkv=False):
+def run_block(g, video, text, emb, wv, wt, last_layer, precision):
     es = 2 if precision == A.COMPUTE_BF16 else 4
-    blk = A.DitBlock(*g.args, g.text_tokens, g.shifted, HEADS, HEAD_DIM, HIDDEN, MLP, last_layer, precision, EPS,
-                     fused_qkv)
+    blk = A.DitBlock(*g.args, g.text_tokens, g.shifted, HEADS, HEAD_DIM, HIDDEN, MLP, last_layer, precision, EPS)
     dv, dt = DeviceBranch(wv, es), DeviceBranch(wt, es)
     bv, bt, be = upload_act(video, es), upload_act(text, es), upload_act(emb, es)
     ov, ot = A.DeviceBuffer(video.size * es), A.DeviceBuffer(text.size * es)
@@ -99,30 +98,7 @@ def test_dit_block_matches_oracle(gpu, precision, shifted, last_layer):
     assert ev <= tol and et <= tol
 
 
-@pytest.mark.parametrize("last_layer", [False, True])
-@pytest.mark.parametrize("shifted", [False, True])
-def test_dit_block_fused_qkv_matches_oracle(gpu, shifted, last_layer):
-    """The bf16 block with fused_qkv: the library's MFMA GEMM projects QKV and
-    applies the q/k RMSNorm and the RoPE rotation (window-local coordinates,
-    so shifted and unshifted windows rotate a token differently) in its
-    epilogue, and the attention reads rotated Q/K. Against the oracle block
-    at the bf16 budget, and against the default path (hipBLASLt projection,
-    norm and RoPE in the attention gather) within twice that budget."""
-    print(f"case dit block fused qkv shifted={shifted} last={last_layer}", flush=True)
-    g, video, text, emb, wv, wt = case(140 + 2 * shifted + last_layer, shifted)
-    got_v, got_t = run_block(g, video, text, emb, wv, wt, last_layer, A.COMPUTE_BF16, fused_qkv=True)
-    def_v, def_t = run_block(g, video, text, emb, wv, wt, last_layer, A.COMPUTE_BF16)
-    ref_v, ref_t = O.dit_block(g, video, text, emb, wv, wt, HEADS, HEAD_DIM, EPS, last_layer, bf16=True)
-    ev, et = rel(got_v, ref_v), rel(got_t, ref_t)
-    dv, dt = rel(got_v, def_v.astype(np.float64)), rel(got_t, def_t.astype(np.float64))
-    print(f"  rel err video {ev:.3g} text {et:.3g}; against the default path {dv:.3g} {dt:.3g}", flush=True)
-    assert ev <= 2e-2 and et <= 2e-2
-    assert dv <= 4e-2 and dt <= 4e-2
-
-
 def test_dit_block_rejects_bad_descriptions(gpu):
-    with pytest.raises(A.AwaError):  # fused_qkv is a bf16-block path
-        A.DitBlock(2, 16, 16, 1, 8, 8, 16, False, HEADS, HEAD_DIM, HIDDEN, MLP, False, A.COMPUTE_F32, EPS, True)
     for kw in ({"head_dim": 64}, {"hidden": 250}, {"precision": 7}):
         args = dict(t=2, h=16, w=16, nt=1, nh=8, nw=8, text_tokens=16, shifted=False, heads=HEADS,
                     head_dim=HEAD_DIM, hidden=HIDDEN, mlp_hidden=MLP, last_layer=False, precision=A.COMPUTE_F32)
@@ -165,15 +141,13 @@ def test_dit_stack_matches_oracle_blocks(gpu):
     assert ev <= 4e-2 and et <= 4e-2
 
 
-@pytest.mark.parametrize("precision,shifted,fused_qkv", [(A.COMPUTE_F32, False, False), (A.COMPUTE_BF16, True, False),
-                                                         (A.COMPUTE_BF16, True, True)])
-def test_dit_block_benchmark_shape(gpu, precision, shifted, fused_qkv):
+@pytest.mark.parametrize("precision,shifted", [(A.COMPUTE_F32, False), (A.COMPUTE_BF16, True)])
+def test_dit_block_benchmark_shape(gpu, precision, shifted):
     """One block at the benchmark workload: latent 9x16x16, windows 3x8x8,
     64 text tokens, hidden 2560 = 20 x 128, SwiGLU 6912; weights N(0, 0.02)
-    (the random init of the benchmark), inputs N(0, 1). Same tolerances; the
-    bf16 block also with the fused QKV projection."""
+    (the random init of the benchmark), inputs N(0, 1). Same tolerances."""
     bf16 = precision == A.COMPUTE_BF16
-    print(f"case dit block benchmark shape bf16={bf16} shifted={shifted} fused_qkv={fused_qkv}", flush=True)
+    print(f"case dit block benchmark shape bf16={bf16} shifted={shifted}", flush=True)
     heads, hidden, mlp = 20, 2560, 6912
     g = geometry((9, 16, 16, 3, 8, 8, 64), shifted)
     rng = np.random.default_rng(2026 + bf16)
@@ -188,7 +162,7 @@ def test_dit_block_benchmark_shape(gpu, precision, shifted, fused_qkv):
     wv, wt = weights(), weights()
     video, text, emb = n(g.source_tokens, hidden, sd=1.0), n(g.text_tokens, hidden, sd=1.0), n(hidden * 6, sd=1.0)
     es = 2 if bf16 else 4
-    blk = A.DitBlock(*g.args, g.text_tokens, g.shifted, heads, HEAD_DIM, hidden, mlp, False, precision, EPS, fused_qkv)
+    blk = A.DitBlock(*g.args, g.text_tokens, g.shifted, heads, HEAD_DIM, hidden, mlp, False, precision, EPS)
     dv, dt = DeviceBranch(wv, es, adjacent_mlp=True), DeviceBranch(wt, es, adjacent_mlp=True)
     bv, bt, be = upload_act(video, es), upload_act(text, es), upload_act(emb, es)
     ov, ot = A.DeviceBuffer(video.size * es), A.DeviceBuffer(text.size * es)

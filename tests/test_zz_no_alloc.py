@@ -1,11 +1,16 @@
 """awa_forward_noalloc: the fused layer with its text rows in the library's
 static per-GPU scratch buffer instead of the plan's workspace. It runs the
 same kernels as awa_forward, so its outputs must be bit-identical to
-awa_forward's on the same inputs. Two calls in a row, the second on a smaller
+awa_forward's on the same inputs. Each no-alloc call runs first, on a fresh
+plan whose work list awa_plan_upload built (awa_plan_desc.heads), and the
+device's free memory is the same before and after it; awa_forward then runs on
+the same plan for the comparison. Two calls in a row, the second on a smaller
 layer, then the clean rejections (text rows beyond the buffer, a plan with no
 work list for the head count)."""
 
 from __future__ import annotations
+
+import ctypes
 
 import numpy as np
 import pytest
@@ -21,6 +26,7 @@ class Layer:
 
     def __init__(self, params, shifted, heads, in_elem, out_elem, seed):
         t, h, w, nt, nh, nw, tx = params
+        self.params, self.shifted = params, shifted
         self.n, self.tx, self.heads, self.out_elem = t * h * w, tx, heads, out_elem
         self.plan = A.Plan(A.LayerParams(t, h, w, nt, nh, nw, tx, shifted), heads=heads)
         self.plan.upload()
@@ -43,13 +49,42 @@ class Layer:
         return (vo.download((self.n * self.heads * HEAD_DIM,), dt), to.download((self.tx * self.heads * HEAD_DIM,), dt))
 
 
+def free_device_bytes() -> int:
+    """hipMemGetInfo's free bytes on the current device."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
+
+
+def warm_kernels(layer: Layer, compute: int) -> None:
+    """Loads the kernels the layer's forward launches (their first launch
+    may load code objects) through awa_forward on a separate plan, so that
+    the no-alloc call's memory check sees only what that call does."""
+    t, h, w, nt, nh, nw, tx = layer.params
+    other = A.Plan(A.LayerParams(t, h, w, nt, nh, nw, tx, layer.shifted), heads=layer.heads)
+    other.upload()
+    _, _, vb, tb = layer.outputs()
+    other.forward(layer.vq_blob, layer.tq_blob, vb, tb, compute)
+    A.synchronize()
+    other.destroy()
+
+
 def run_both(layer: Layer, compute: int):
+    """The no-alloc call first (the plan's work list comes from
+    awa_plan_upload), then awa_forward on the same plan and inputs."""
+    warm_kernels(layer, compute)
     vo_a, to_a, vb_a, tb_a = layer.outputs()
     vo_b, to_b, vb_b, tb_b = layer.outputs()
-    layer.plan.forward(layer.vq_blob, layer.tq_blob, vb_a, tb_a, compute)
+    A.synchronize()
+    before = free_device_bytes()
     rc = layer.plan.forward_noalloc(layer.vq_blob, layer.tq_blob, vb_b, tb_b, compute)
     A.synchronize()
+    after = free_device_bytes()
     assert rc == A.AWA_OK, A.lib().awa_last_error()
+    assert after == before, f"the no-alloc call changed free device memory by {before - after} bytes"
+    layer.plan.forward(layer.vq_blob, layer.tq_blob, vb_a, tb_a, compute)
+    A.synchronize()
     return layer.read(vo_a, to_a), layer.read(vo_b, to_b)
 
 
