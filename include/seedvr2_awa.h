@@ -107,7 +107,9 @@ typedef struct awa_plan awa_plan;
 
 const char* awa_last_error(void);
 int awa_device_count(int* count);
-/* Selects the device for the calling thread and caches its properties. */
+/* Selects the device for the calling thread and sets up the device's static
+ * scratch buffer of awa_forward_noalloc (its memory is reserved then, once per
+ * device, and held until the process ends). */
 int awa_runtime_init(int device);
 int awa_malloc(void** ptr, size_t bytes);
 int awa_free(void* ptr);
@@ -185,8 +187,10 @@ int awa_forward(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob*
  * awa_plan_upload when awa_plan_desc.heads names it, or by an earlier
  * awa_forward with that head count; else AWA_ERR_INVALID). Every call on a
  * GPU uses that GPU's one buffer, which keeps the last call's contents:
- * calls that overlap on one GPU (other streams or threads) race. Same blobs,
- * compute modes and results as awa_forward. */
+ * calls that overlap on one GPU (other streams or threads) race. The buffer
+ * is set up by awa_runtime_init for its device (else by the first call on a
+ * device), after which a call reserves no device memory. Same blobs, compute
+ * modes and results as awa_forward. */
 #define AWA_NOALLOC_SCRATCH_BYTES (32u << 20)
 int awa_forward_noalloc(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv,
                         const awa_blob* video_out, const awa_blob* text_out, int compute, void* stream);

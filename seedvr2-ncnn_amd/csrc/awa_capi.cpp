@@ -392,7 +392,9 @@ int awa_runtime_init(int device)
     if (device < 0 || device >= n)
         return fail(AWA_ERR_INVALID, "device index out of range");
     HIP_TRY(hipSetDevice(device), "hipSetDevice");
-    return AWA_OK;
+    // The no-alloc entry point's static scratch array is set up here, once
+    // per device, so that its first call reserves nothing.
+    return awa::noalloc_setup();
 }
 
 int awa_malloc(void** ptr, size_t bytes)

@@ -31,4 +31,9 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
                   const awa_blob* video_out, const awa_blob* text_out, int compute, hipStream_t stream,
                   hipEvent_t after_attention, const Scratch* scratch = nullptr);
 
+// Resolves the current device's address of awa_forward_noalloc's static
+// scratch array (once per device); AWA_ERR_DEVICE with the reason set if the
+// runtime cannot.
+int noalloc_setup();
+
 } // namespace awa

@@ -9,7 +9,10 @@
 //
 // In host code the array's name is only a host-side stand-in: its device
 // address on each GPU comes from hipGetSymbolAddress, taken once per device
-// with that device current, and only that address is handed to kernels.
+// with that device current (by awa_runtime_init, or by the first no-alloc
+// call on a device that was not set up through it), and only that address
+// is handed to kernels. Resolving the symbol loads the array's code object,
+// which is when the runtime reserves the array's memory on that device.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -53,6 +56,16 @@ void* device_scratch()
 }
 
 } // namespace
+
+namespace awa
+{
+
+int noalloc_setup()
+{
+    return device_scratch() ? AWA_OK : AWA_ERR_DEVICE;
+}
+
+} // namespace awa
 
 extern "C" int awa_forward_noalloc(const awa_plan* plan, const awa_blob* video_qkv, const awa_blob* text_qkv,
                                    const awa_blob* video_out, const awa_blob* text_out, int compute, void* stream)
