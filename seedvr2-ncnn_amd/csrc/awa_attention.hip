@@ -48,6 +48,23 @@ using namespace dev;
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
+// Bytes of one wave's output stage: 32 rows of 128 bf16 features and 32 row
+// pointers.
+constexpr int kOutStageWaveBytes = 32 * kHeadDim * 2 + 32 * 8;
+
+// Static LDS of a kernel instance: the K tile (keys x padded head_dim) and the
+// V tile (bf16: keys x padded head_dim; fp32: head_dim x padded keys), 64
+// bf16 keys or 32 fp32 keys, double-buffered in the fp32 pipeline; the bf16
+// kernels' output stage reuses the space and may need more.
+constexpr int static_lds_bytes(bool bf16, int variant)
+{
+    const int tiles = bf16 ? 64 * (kHeadDim + 8) * 2 + 64 * (kHeadDim + 32) * 2
+                           : 32 * (kHeadDim + 4) * 4 + kHeadDim * (32 + 4) * 4;
+    const int buffered = (variant == kVariantWidePipe ? 2 : 1) * tiles;
+    const int waves = variant == kVariantNarrow ? 4 : 8;
+    return bf16 && buffered < waves * kOutStageWaveBytes ? waves * kOutStageWaveBytes : buffered;
+}
+
 // Variants (AttentionLaunch::variant):
 //   kVariantNarrow: 4 waves (128 query rows), single-buffered K/V tiles of 64
 //     (bf16) or 32 (fp32) keys, two barriers per tile; the LDS footprint stays
@@ -84,8 +101,18 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
     constexpr int kVBytes = (BF16 ? KT : kHeadDim) * kVPitch * kElem;
     constexpr int kBlocks = KT / 32; // 32-key score blocks per tile
 
-    __shared__ __attribute__((aligned(16))) unsigned char k_lds[kBufs * kKBytes];
-    __shared__ __attribute__((aligned(16))) unsigned char v_lds[kBufs * kVBytes];
+    // bf16 fused kernels stage each wave's output rows through LDS after the
+    // loop (see the store below): 32 rows of 256 bytes plus 32 row pointers
+    // per wave, in the tile buffers' space.
+    constexpr bool kStageOut = BF16 && FUSED;
+    constexpr int kStaticBytes = static_lds_bytes(BF16, VARIANT);
+    static_assert(kStaticBytes >= kBufs * (kKBytes + kVBytes), "tiles fit the static LDS");
+    static_assert(!kStageOut || kStaticBytes >= (kThreads / 64) * kOutStageWaveBytes, "output stage fits");
+    // With the output stage, one array holds the K tiles, then the V tiles.
+    __shared__ __attribute__((aligned(16))) unsigned char k_lds[kStageOut ? kStaticBytes : kBufs * kKBytes];
+    __shared__ __attribute__((aligned(16))) unsigned char v_lds_own[kStageOut ? 16 : kBufs * kVBytes];
+    unsigned char* const v_lds = kStageOut ? k_lds + kBufs * kKBytes : v_lds_own;
+    unsigned char* const tile_lds = k_lds;
     // Dynamic LDS: the RoPE table (fused mode; its coordinates plus an
     // identity row), then the row table.
     extern __shared__ __attribute__((aligned(16))) unsigned char dyn_lds[];
@@ -831,6 +858,74 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
         }
     }
 
+    if constexpr (kStageOut)
+    {
+        // ---- store through LDS: the lane pair (col, half) holds row col's
+        // features db*32 + 8*g + 4*half + [0,4); the wave writes its rows as
+        // bf16 into its own LDS region (16-byte chunk c of row i at position
+        // c ^ (i & 15): conflict-free both ways), then reads them back 16
+        // bytes a lane, 16 lanes a row, and writes whole 256-byte rows. Rows
+        // with an fp32 destination (fp32 outputs or text rows) are stored
+        // directly; rows past the window are not stored. ----
+        if (!wave_active)
+            return;
+        const float inv = 1.f / sum_xor32(row_sum);
+        unsigned char* const region = tile_lds + wave * kOutStageWaveBytes;
+        uint16_t* const rows_lds = reinterpret_cast<uint16_t*>(region);
+        unsigned long long* const dst_lds = reinterpret_cast<unsigned long long*>(region + 32 * 256);
+        uint16_t* dst16 = nullptr;
+        if (q_valid)
+        {
+            const RowRef r = decode(qi);
+            if (!r.text)
+            {
+                TOut* dst = static_cast<TOut*>(p.video_out.data) + r.t * p.video_out.ts + r.h * p.video_out.hs +
+                            r.w * p.video_out.ws + head_off;
+                if constexpr (sizeof(TOut) == 2)
+                    dst16 = dst;
+                else
+                    store_row(dst, o, inv, half);
+            }
+            else
+            {
+                // Text partials in the text output's type (bf16 rows are
+                // rounded before the mean, as in the reference's bf16 layer).
+                const long long off =
+                    ((static_cast<long long>(item.window) * p.text_tokens + r.k) * p.heads + head) * kHeadDim;
+                if (p.text_partial_elemsize == 2)
+                    dst16 = static_cast<uint16_t*>(p.text_partials) + off;
+                else
+                    store_row(static_cast<float*>(p.text_partials) + off, o, inv, half);
+            }
+        }
+#pragma unroll
+        for (int db = 0; db < 4; db++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+            {
+                const int chunk = (4 * db + g) ^ (col & 15);
+                *reinterpret_cast<uint2*>(rows_lds + col * kHeadDim + 8 * chunk + 4 * half) =
+                    make_uint2(cvt_pk_bf16(o[db][4 * g] * inv, o[db][4 * g + 1] * inv),
+                               cvt_pk_bf16(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv));
+            }
+        if (half == 0)
+            dst_lds[col] = reinterpret_cast<unsigned long long>(dst16);
+        // The wave reads what its own lanes wrote.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int chunk = lane & 15;
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+        {
+            const int row = 4 * j + (lane >> 4);
+            const uint4 v = *reinterpret_cast<const uint4*>(rows_lds + row * kHeadDim + 8 * (chunk ^ (row & 15)));
+            uint16_t* const d = reinterpret_cast<uint16_t*>(dst_lds[row]);
+            if (d)
+                *reinterpret_cast<uint4*>(d + 8 * chunk) = v;
+        }
+        return;
+    }
     if (!q_valid)
         return;
     const float inv = 1.f / sum_xor32(row_sum);
@@ -869,11 +964,7 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
 
 size_t attention_static_lds(bool bf16_mfma, int variant)
 {
-    // K tile (keys x padded head_dim) and transposed V tile (head_dim x padded
-    // keys): 64 bf16 keys or 32 fp32 keys; double-buffered in the pipeline.
-    const size_t tiles = bf16_mfma ? 64 * (kHeadDim + 8) * 2 + 64 * (kHeadDim + 32) * 2
-                                   : 32 * (kHeadDim + 4) * 4 + kHeadDim * (32 + 4) * 4;
-    return (variant == kVariantWidePipe ? 2 : 1) * tiles;
+    return static_lds_bytes(bf16_mfma, variant);
 }
 
 size_t attention_dynamic_lds(const AttentionLaunch& p)
