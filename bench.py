@@ -189,8 +189,23 @@ CONFIGS = {
     "mixed_step_9x16x16": ((9, 16, 16), (3, 8, 8), "mixed", ("unshifted", "shifted")),
     "bf16_clip_512_9x32x32": ((9, 32, 32), (3, 8, 8), "bf16", ("unshifted", "shifted")),
     "bf16_clip_121f_31x16x16": ((31, 16, 16), (8, 8, 8), "bf16", ("unshifted", "shifted")),
+    # The production 256x256 image layer (windows (4, 3, 3): one 16 x 16
+    # window of 256 + 64 rows, 20 units; the fp32 layer splits its keys).
+    "fp32_production_256": ((1, 16, 16), (4, 3, 3), "fp32", ("unshifted",)),
+    "bf16_production_256": ((1, 16, 16), (4, 3, 3), "bf16", ("unshifted",)),
 }
 MALL_BYTES = 256 * 1024 * 1024
+
+
+def key_segments(A, grid, windows, shifted: bool, label: str) -> int:
+    """Key segments per (window, head) unit the layer's attention uses (1:
+    one workgroup per query block; more: the keys split over workgroups and
+    combined by a second kernel, which the layer time includes)."""
+    plan = A.Plan(A.LayerParams(*grid, *windows, TEXT, shifted))
+    plan.upload()
+    s = plan.attention_split(HEADS, A.COMPUTE_F32 if label == "fp32" else A.COMPUTE_BF16)
+    plan.destroy()
+    return s
 
 
 def config_measurements(A, stream, steps: int = 10, profile_steps: int = 5) -> dict:
@@ -275,7 +290,9 @@ def config_measurements(A, stream, steps: int = 10, profile_steps: int = 5) -> d
                         "layer_tflops": round(fl / (l_ms * 1e-3) / 1e12, 2),
                         "pct_bf16_peak": round(100.0 * fl / (k_ms * 1e-3) / PEAK_BF16, 2),
                         "roofline_frac": round(fl / (k_ms * 1e-3) / roof, 4),
+                        "layer_roofline_frac": round(fl / (l_ms * 1e-3) / roof, 4),
                         "roof": "hbm" if roof < peak else ("mfma_fp32" if label == "fp32" else "mfma_bf16"),
+                        "key_segments": key_segments(A, grid, windows, kind == "shifted", label),
                     }
             res[regime] = entry
         out[name] = res

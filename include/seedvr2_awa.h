@@ -158,6 +158,16 @@ int awa_plan_text_positions(const awa_plan* plan, int* out);
 int awa_plan_rope_table(const awa_plan* plan, float* out);
 /* Copies the plan's device tables to the current device (upload_model). */
 int awa_plan_upload(awa_plan* plan, void* stream);
+/* No counterpart in the reference. The number of key segments the fused and
+ * staged attention of this plan use for `heads` heads in `compute` mode: 1, or
+ * S > 1 (AWA_COMPUTE_F32 only) when the layer's (window, head) units are long
+ * but too few to fill the device, so that each unit's keys are split over S
+ * workgroups and a second kernel combines the segments (in place of the
+ * text-mean kernel). Builds the plan's work
+ * lists for that head count if they are missing (as awa_plan_upload does with
+ * awa_plan_desc.heads); SEEDVR2_AWA_SPLIT=0 in the environment when they are
+ * built turns splitting off. For workspace sizing and tests. */
+int awa_plan_attention_split(const awa_plan* plan, int heads, int compute, int* split);
 
 /* ---- forward entry points ---- */
 

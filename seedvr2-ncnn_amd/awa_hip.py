@@ -35,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "awa_event_synchronize", "awa_event_elapsed_ms", "awa_fill_normal", "awa_fill_normal_scaled", "awa_plan_create", "awa_plan_destroy",
     "awa_plan_info_get", "awa_plan_windows", "awa_plan_sequence_index", "awa_plan_cu_seqlens",
     "awa_plan_video_positions", "awa_plan_text_positions", "awa_plan_rope_table", "awa_plan_upload",
+    "awa_plan_attention_split",
     "awa_qkv_shape", "awa_forward", "awa_forward_noalloc", "awa_forward_qknorm", "awa_rmsnorm", "awa_qkv_concat", "awa_pack", "awa_mmrope",
     "awa_window_attention", "awa_unpack", "awa_cast",
     "awa_stack_create", "awa_stack_destroy", "awa_stack_run", "awa_stack_set_profiling", "awa_stack_set_graph", "awa_stack_block_times",
@@ -147,6 +148,7 @@ def lib() -> ctypes.CDLL:
             getattr(L, name).argtypes = [vp, vp]
         L.awa_plan_rope_table.argtypes = [vp, vp]
         L.awa_plan_upload.argtypes = [vp, vp]
+        L.awa_plan_attention_split.argtypes = [vp, i, i, ctypes.POINTER(i)]
         bp = ctypes.POINTER(AwaBlob)
         L.awa_forward.argtypes = [vp, bp, bp, bp, bp, i, vp]
         L.awa_forward_noalloc.argtypes = [vp, bp, bp, bp, bp, i, vp]
@@ -386,6 +388,12 @@ class Plan:
 
     def upload(self, stream: Optional[Stream] = None) -> None:
         check(lib().awa_plan_upload(self.h, _s(stream)), "awa_plan_upload")
+
+    def attention_split(self, heads: int, compute: int) -> int:
+        """Key segments per (window, head) unit of this layer (1: not split)."""
+        s = ctypes.c_int()
+        check(lib().awa_plan_attention_split(self.h, heads, compute, ctypes.byref(s)), "awa_plan_attention_split")
+        return s.value
 
     # forward entry points (blobs are AwaBlob descriptors of device memory)
     def forward(self, video_qkv: AwaBlob, text_qkv: AwaBlob, video_out: AwaBlob, text_out: AwaBlob,

@@ -133,6 +133,11 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
     const int half = lane >> 5;
     const int head_off = head * kHeadDim;
     const int tiles = (L + KT - 1) / KT;
+    // Key tiles of this item: all of them, or one segment of a split layer
+    // (its key range starts at a multiple of 64 keys; the pipelined fp32
+    // variant is never split).
+    const int t_begin = PIPE ? 0 : item.key0 / KT;
+    const int t_end = PIPE ? tiles : min(tiles, (item.key1 + KT - 1) / KT);
     const int table_rows = (p.max_window_tokens + 63) & ~63;
 
     // Wave-uniform scalars read once from the kernel arguments (plain values,
@@ -414,7 +419,7 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
     // ---- prologue: tile 0's loads, the RoPE table into LDS (plus an
     // identity row after the last coordinate), Q rotated and scaled in
     // registers ----
-    load_tile(0);
+    load_tile(t_begin);
     // The pipeline also stages K(1) before its first step.
     uint32_t k1[PIPE ? kKRows * kRW : 1];
     if constexpr (PIPE)
@@ -638,10 +643,10 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
         if constexpr (kRel)
         {
             // tile_max is relative to row_max.
-            if (tile == 0 || __any(tile_max > kRescaleThreshold))
+            if (tile == t_begin || __any(tile_max > kRescaleThreshold))
             {
-                const float delta = tile == 0 ? tile_max : fmaxf(tile_max, 0.f);
-                if (tile != 0)
+                const float delta = tile == t_begin ? tile_max : fmaxf(tile_max, 0.f);
+                if (tile != t_begin)
                 {
                     const float alpha = __builtin_amdgcn_exp2f(-delta);
                     row_sum *= alpha;
@@ -841,11 +846,11 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
     {
         // Step t: stage tile t into LDS, refill the registers with tile t+1's
         // loads, then scores, softmax and PV of tile t.
-        for (int tile = 0; tile < tiles; tile++)
+        for (int tile = t_begin; tile < t_end; tile++)
         {
             store_tile(tile, 0);
             __syncthreads();
-            if (tile + 1 < tiles)
+            if (tile + 1 < t_end)
                 load_tile(tile + 1);
             if (wave_active)
             {
@@ -858,6 +863,21 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
         }
     }
 
+    if (p.split > 1)
+    {
+        // ---- one key segment of a split layer: the unnormalised row (relative
+        // to the running maximum) and (maximum, probability sum), for
+        // launch_split_merge ----
+        const float l = sum_xor32(row_sum);
+        if (!q_valid)
+            return;
+        const long long slot =
+            (static_cast<long long>(win.seq_start + qi) * p.heads + head) * p.split + item.seg;
+        store_row(p.split_o + slot * kHeadDim, o, 1.f, half);
+        if (half == 0)
+            p.split_ml[slot] = make_float2(row_max, l);
+        return;
+    }
     if constexpr (kStageOut)
     {
         // ---- store through LDS: the lane pair (col, half) holds row col's

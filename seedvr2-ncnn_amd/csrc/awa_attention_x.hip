@@ -139,6 +139,9 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
     const int half = lane >> 5;
     const int head_off = head * kHeadDim;
     const int tiles = (L + KT - 1) / KT;
+    // Key tiles of this item: all of them, or one segment of a split layer.
+    const int t_begin = item.key0 / KT;
+    const int t_end = min(tiles, (item.key1 + KT - 1) / KT);
     const int table_rows = (p.max_window_tokens + 63) & ~63;
 
     const TIn* const video_base = static_cast<const TIn*>(p.video.data);
@@ -321,7 +324,7 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
     // ---- prologue: tile 0's loads (8-wave form), the RoPE table (plus an
     // identity row) and the K gammas into LDS ----
     if constexpr (WIDE)
-        load_tile(0);
+        load_tile(t_begin);
     uint32_t q_code = 0;
     if constexpr (FUSED)
     {
@@ -501,10 +504,10 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
         for (int i = 1; i < 16; i++)
             tile_max = fmaxf(tile_max, s[i]);
         tile_max = max_xor32(tile_max);
-        if (tile == 0 || __any(tile_max > kRescaleThreshold))
+        if (tile == t_begin || __any(tile_max > kRescaleThreshold))
         {
-            const float delta = tile == 0 ? tile_max : fmaxf(tile_max, 0.f);
-            if (tile != 0)
+            const float delta = tile == t_begin ? tile_max : fmaxf(tile_max, 0.f);
+            if (tile != t_begin)
             {
                 const float alpha = __builtin_amdgcn_exp2f(-delta);
                 row_sum *= alpha;
@@ -587,21 +590,21 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
         // (the second wave on each SIMD) stage first, so that one wave's VALU
         // staging runs while the other's MFMAs hold the matrix core.
         const bool stage_first = wave >= 4;
-        store_k(0, 0);
+        store_k(t_begin, 0);
         store_v(0);
-        if (tiles > 1)
-            load_tile(1);
+        if (t_begin + 1 < t_end)
+            load_tile(t_begin + 1);
         __syncthreads();
-        for (int tile = 0; tile < tiles; tile++)
+        for (int tile = t_begin; tile < t_end; tile++)
         {
-            const int buf = tile & 1;
-            const bool next = tile + 1 < tiles;
+            const int buf = (tile - t_begin) & 1;
+            const bool next = tile + 1 < t_end;
             auto stage = [&]() {
                 if (next)
                 {
                     store_k(tile + 1, buf ^ 1);
                     store_v(buf ^ 1);
-                    if (tile + 2 < tiles)
+                    if (tile + 2 < t_end)
                         load_tile(tile + 2);
                 }
             };
@@ -612,7 +615,7 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
                 f32x16 f;
                 scores_hi(buf, f);
                 scores_lo(buf, f);
-                softmax_pv(tile, buf, f, !next);
+                softmax_pv(tile, buf, f, tile == tiles - 1);
             }
             if (!stage_first)
                 stage();
@@ -623,7 +626,7 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
     {
         // Step t: load, stage, barrier, compute, barrier (the other workgroup
         // on the CU covers the load latency).
-        for (int tile = 0; tile < tiles; tile++)
+        for (int tile = t_begin; tile < t_end; tile++)
         {
             load_tile(tile);
             store_k(tile, 0);
@@ -640,6 +643,21 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
         }
     }
 
+    if (p.split > 1)
+    {
+        // One key segment of a split layer: the unnormalised row (relative to
+        // the running maximum) and (maximum, probability sum), for
+        // launch_split_merge.
+        const float l = sum_xor32(row_sum);
+        if (!q_valid)
+            return;
+        const long long slot =
+            (static_cast<long long>(win.seq_start + qi) * p.heads + head) * p.split + item.seg;
+        store_row(p.split_o + slot * kHeadDim, o, 1.f, half);
+        if (half == 0)
+            p.split_ml[slot] = make_float2(row_max, l);
+        return;
+    }
     if (!q_valid)
         return;
     const float inv = 1.f / sum_xor32(row_sum);

@@ -219,8 +219,20 @@ int launch_variant(int compute, const awa_plan& plan, awa::AttentionLaunch& p)
                                          " rows needs " + std::to_string(lds(p.variant, p)) +
                                          " bytes of LDS per workgroup, more than " +
                                          std::to_string(awa::kWorkgroupLds));
-    p.work = p.variant != awa::kVariantNarrow ? plan.work_wide : plan.work;
-    p.work_count = p.variant != awa::kVariantNarrow ? plan.work_wide_count : plan.work_count;
+    // Split layers: the key-segment lists, for the exact-score fp32 kernel.
+    const bool wide = p.variant != awa::kVariantNarrow;
+    const int split = compute != AWA_COMPUTE_F32 ? 1 : (wide ? plan.split_wide : plan.split);
+    p.split = split;
+    if (split > 1)
+    {
+        p.work = wide ? plan.work_wide_split : plan.work_split;
+        p.work_count = wide ? plan.work_wide_split_count : plan.work_split_count;
+    }
+    else
+    {
+        p.work = wide ? plan.work_wide : plan.work;
+        p.work_count = wide ? plan.work_wide_count : plan.work_count;
+    }
     return AWA_OK;
 }
 
@@ -245,7 +257,61 @@ std::vector<std::pair<int, int>> split_rows(int L, int rows_per_block)
     return items;
 }
 
-std::vector<awa::WorkItem> build_work(const awa_plan& plan, int heads, int rows_per_block)
+// Compute units of the current device (256 on MI355X), cached per device.
+int device_cus()
+{
+    static std::mutex m;
+    static int cus[64] = {};
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64)
+        return 256;
+    std::lock_guard<std::mutex> lock(m);
+    if (!cus[device])
+    {
+        hipDeviceProp_t prop{};
+        cus[device] = hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0
+                          ? prop.multiProcessorCount
+                          : 256;
+    }
+    return cus[device];
+}
+
+// Key segments per unit of the exact-score fp32 kernel for query blocks of
+// rows_per_block rows: 1 (no split), or, when the layer's work items fill
+// fewer than half of the device's concurrent workgroup slots (two 4-wave or
+// one 8-wave workgroup per CU) and every unit has at least kMinSplitTiles
+// 64-key tiles, the most segments (at most 8) that still fit those slots with
+// at least one tile per segment in every unit. The production 256x256 layer
+// (20 units of 320 rows) then uses the whole device. Shorter units, and the
+// bf16 kernel, whose items are dominated by their start-up, lose more to the
+// fp32 segment rows and the combining kernel than they gain (measured on the
+// 1x16x16 image, 2x16x16 clip and production layers). The environment
+// variable SEEDVR2_AWA_SPLIT=0, read when a plan builds its work lists, turns
+// splitting off.
+constexpr int kMaxSplit = 8;
+constexpr int kMinSplitTiles = 4;
+int split_factor(const awa_plan& plan, int heads, int rows_per_block)
+{
+    const char* env = std::getenv("SEEDVR2_AWA_SPLIT");
+    if (env && std::string(env) == "0")
+        return 1;
+    long long items = 0;
+    int min_tiles = 1 << 30;
+    for (const awa::WindowDesc& w : plan.window_descs)
+    {
+        const int L = w.video_tokens + plan.text_tokens;
+        items += (L + rows_per_block - 1) / rows_per_block;
+        min_tiles = std::min(min_tiles, (L + 63) / 64);
+    }
+    items *= heads;
+    const long long slots = (rows_per_block == awa::kQueryRows ? 2LL : 1LL) * device_cus();
+    if (items <= 0 || 2 * items > slots || min_tiles < kMinSplitTiles)
+        return 1;
+    const long long s = std::min<long long>({kMaxSplit, min_tiles, slots / items});
+    return s >= 2 ? static_cast<int>(s) : 1;
+}
+
+std::vector<awa::WorkItem> build_work(const awa_plan& plan, int heads, int rows_per_block, int split)
 {
     struct Unit
     {
@@ -268,13 +334,18 @@ std::vector<awa::WorkItem> build_work(const awa_plan& plan, int heads, int rows_
     {
         const int x = static_cast<int>(std::min_element(load.begin(), load.end()) - load.begin());
         load[x] += u.cost;
+        // Segment s of a unit: its 64-key tiles [s T / split, (s + 1) T / split).
+        const int L = plan.window_descs[u.window].video_tokens + plan.text_tokens;
+        const int T = (L + 63) / 64;
         for (const auto& it : u.items)
-            lists[x].push_back({plan.window_descs[u.window], u.window, u.head, it.first, it.second});
+            for (int s = 0; s < split; s++)
+                lists[x].push_back({plan.window_descs[u.window], u.window, u.head, it.first, it.second,
+                                    64 * (s * T / split), std::min(L, 64 * ((s + 1) * T / split)), s, 0});
     }
     size_t longest = 0;
     for (const auto& l : lists)
         longest = std::max(longest, l.size());
-    std::vector<awa::WorkItem> work(longest * kXcds, awa::WorkItem{awa::WindowDesc{}, -1, 0, 0, 0});
+    std::vector<awa::WorkItem> work(longest * kXcds, awa::WorkItem{awa::WindowDesc{}, -1, 0, 0, 0, 0, 0, 0, 0});
     for (int x = 0; x < kXcds; x++)
         for (size_t j = 0; j < lists[x].size(); j++)
             work[j * kXcds + x] = lists[x][j];
@@ -284,46 +355,73 @@ std::vector<awa::WorkItem> build_work(const awa_plan& plan, int heads, int rows_
     return work;
 }
 
-// Ensures the plan's work list for `heads` and a text-partials buffer of at
-// least `partial_bytes` exist on the device. The caller holds plan.mutex, and
-// keeps holding it until the kernels that read the work list are enqueued, so
-// that no other call replaces the list in between.
-int ensure_workspace_locked(const awa_plan& plan, int heads, size_t partial_bytes)
+// Ensures the plan's work lists for `heads` exist on the device: query
+// blocks of 128 and of 256 rows, each also split into key segments when
+// split_factor says so. The caller holds plan.mutex, and keeps holding it
+// until the kernels that read the lists are enqueued, so that no other call
+// replaces them in between.
+int ensure_work_locked(const awa_plan& plan, int heads)
 {
-    if (plan.work_heads != heads || !plan.work)
-    {
-        for (const bool wide : {false, true})
+    if (plan.work_heads == heads && plan.work)
+        return AWA_OK;
+    for (const bool wide : {false, true})
+        for (const bool split : {false, true})
         {
-            awa::WorkItem*& dst = wide ? plan.work_wide : plan.work;
-            int& count = wide ? plan.work_wide_count : plan.work_count;
-            const std::vector<awa::WorkItem> work =
-                build_work(plan, heads, wide ? awa::kWideQueryRows : awa::kQueryRows);
+            awa::WorkItem*& dst = wide ? (split ? plan.work_wide_split : plan.work_wide)
+                                       : (split ? plan.work_split : plan.work);
+            int& count = wide ? (split ? plan.work_wide_split_count : plan.work_wide_count)
+                              : (split ? plan.work_split_count : plan.work_count);
+            const int rows = wide ? awa::kWideQueryRows : awa::kQueryRows;
+            const int factor = split ? split_factor(plan, heads, rows) : 1;
+            if (split)
+                (wide ? plan.split_wide : plan.split) = factor;
             if (dst)
             {
                 (void)hipFree(dst);
                 dst = nullptr;
             }
+            count = 0;
+            if (split && factor == 1)
+                continue;
+            const std::vector<awa::WorkItem> work = build_work(plan, heads, rows, factor);
             if (hipMalloc(&dst, std::max<size_t>(work.size(), 1) * sizeof(awa::WorkItem)) != hipSuccess)
                 return fail(AWA_ERR_ALLOC, "work list allocation failed");
             HIP_TRY(hipMemcpy(dst, work.data(), work.size() * sizeof(awa::WorkItem), hipMemcpyHostToDevice),
                     "work list upload");
             count = static_cast<int>(work.size());
         }
-        plan.work_heads = heads;
-    }
-    if (partial_bytes > plan.text_partials_bytes)
-    {
-        if (plan.text_partials)
-        {
-            (void)hipFree(plan.text_partials);
-            plan.text_partials = nullptr;
-            plan.text_partials_bytes = 0;
-        }
-        if (hipMalloc(&plan.text_partials, partial_bytes) != hipSuccess)
-            return fail(AWA_ERR_ALLOC, "text partial workspace allocation failed");
-        plan.text_partials_bytes = partial_bytes;
-    }
+    plan.work_heads = heads;
     return AWA_OK;
+}
+
+// Ensures the plan's workspace (text rows of an unsplit layer, or the key
+// segments of a split one) holds at least `bytes`. Caller holds plan.mutex.
+int ensure_partials_locked(const awa_plan& plan, size_t bytes)
+{
+    if (bytes <= plan.text_partials_bytes)
+        return AWA_OK;
+    if (plan.text_partials)
+    {
+        (void)hipFree(plan.text_partials);
+        plan.text_partials = nullptr;
+        plan.text_partials_bytes = 0;
+    }
+    if (hipMalloc(&plan.text_partials, bytes) != hipSuccess)
+        return fail(AWA_ERR_ALLOC, "attention workspace allocation failed");
+    plan.text_partials_bytes = bytes;
+    return AWA_OK;
+}
+
+// Bytes of a split layer's segments: per packed row, head and segment the
+// unnormalised row (head_dim fp32) and its (maximum, sum), the rows first.
+size_t split_o_bytes(const awa_plan& plan, int heads, int split)
+{
+    return static_cast<size_t>(plan.sequence_tokens) * heads * split * awa::kHeadDim * sizeof(float);
+}
+
+size_t split_bytes(const awa_plan& plan, int heads, int split)
+{
+    return split_o_bytes(plan, heads, split) + static_cast<size_t>(plan.sequence_tokens) * heads * split * 8;
 }
 
 template <typename T>
@@ -357,7 +455,12 @@ void free_device(awa_plan& plan)
     release(plan.dev.rope_cs);
     release(plan.work);
     release(plan.work_wide);
+    release(plan.work_split);
+    release(plan.work_wide_split);
     plan.work_wide_count = 0;
+    plan.work_split_count = 0;
+    plan.work_wide_split_count = 0;
+    plan.split = plan.split_wide = 1;
     release(plan.text_partials);
     plan.text_partials_bytes = 0;
     plan.work_heads = 0;
@@ -685,7 +788,7 @@ int upload_plan(awa_plan* plan, void* stream)
     if (rc != AWA_OK || plan->heads_hint <= 0)
         return rc;
     std::lock_guard<std::mutex> lock(plan->mutex);
-    return ensure_workspace_locked(*plan, plan->heads_hint, 0);
+    return ensure_work_locked(*plan, plan->heads_hint);
 }
 
 } // namespace
@@ -695,6 +798,27 @@ extern "C" {
 int awa_plan_upload(awa_plan* plan, void* stream)
 {
     return upload_plan(plan, stream);
+}
+
+int awa_plan_attention_split(const awa_plan* plan, int heads, int compute, int* split)
+{
+    int rc = check_plan_uploaded(plan);
+    if (rc != AWA_OK)
+        return rc;
+    if (!split || heads <= 0 || !valid_compute(compute))
+        return fail(AWA_ERR_INVALID, "invalid argument");
+    std::lock_guard<std::mutex> lock(plan->mutex);
+    if ((rc = ensure_work_locked(*plan, heads)) != AWA_OK)
+        return rc;
+    awa::AttentionLaunch p{};
+    p.fused = true;
+    p.bf16_mfma = compute == AWA_COMPUTE_BF16;
+    p.rope_coords = plan->rope_coords;
+    p.max_window_tokens = plan->max_window_tokens;
+    if ((rc = launch_variant(compute, *plan, p)) != AWA_OK)
+        return rc;
+    *split = p.split;
+    return AWA_OK;
 }
 
 // ---- forward ----
@@ -776,33 +900,18 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
             return fail(AWA_ERR_INVALID, "norm eps must be finite and non-negative");
     }
 
-    void* partials = nullptr;
     // Held until both kernels are enqueued: they read the plan's work list
-    // and text workspace, which a call with another head count replaces.
+    // and workspace, which a call with another head count replaces.
     std::lock_guard<std::mutex> lock(plan->mutex);
     if (scratch)
     {
-        // No allocation: the text rows in the caller's buffer, the work list
-        // already on the device.
-        const size_t need = plan->windows.size() * static_cast<size_t>(plan->text_tokens) * vl.heads *
-                            vl.head_dim * static_cast<size_t>(text_out->elemsize);
-        if (need > scratch->bytes)
-            return fail(AWA_ERR_INVALID, "text rows of this layer need " + std::to_string(need) +
-                                             " bytes, more than the no-alloc scratch buffer's " +
-                                             std::to_string(scratch->bytes));
+        // No allocation: the work list must already be on the device.
         if (plan->work_heads != vl.heads || !plan->work)
             return fail(AWA_ERR_INVALID, "plan has no work list for " + std::to_string(vl.heads) +
                                              " heads: create it with awa_plan_desc.heads set, or run awa_forward once");
-        partials = scratch->ptr;
     }
-    else
-    {
-        const size_t partial_bytes = plan->windows.size() * static_cast<size_t>(plan->text_tokens) * vl.heads *
-                                     vl.head_dim * sizeof(float);
-        if ((rc = ensure_workspace_locked(*plan, vl.heads, partial_bytes)) != AWA_OK)
-            return rc;
-        partials = plan->text_partials;
-    }
+    else if ((rc = ensure_work_locked(*plan, vl.heads)) != AWA_OK)
+        return rc;
 
     awa::AttentionLaunch p{};
     p.fused = true;
@@ -810,7 +919,6 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
     p.video = {video_qkv->data, vl.token_stride, vl.qkv_stride, elem};
     p.text = {text_qkv->data, tl.token_stride, tl.qkv_stride, elem};
     p.video_out = sink;
-    p.text_partials = partials;
     p.text_partial_elemsize = static_cast<int>(text_out->elemsize);
     if (norm)
     {
@@ -827,6 +935,34 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
     p.max_window_tokens = plan->max_window_tokens;
     if ((rc = launch_variant(compute, *plan, p)) != AWA_OK)
         return rc;
+    // Workspace: the per-window text rows, or a split layer's key segments;
+    // in the caller's scratch buffer (no allocation) or the plan's.
+    const size_t need = p.split > 1 ? split_bytes(*plan, vl.heads, p.split)
+                                    : plan->windows.size() * static_cast<size_t>(plan->text_tokens) * vl.heads *
+                                          vl.head_dim * static_cast<size_t>(text_out->elemsize);
+    void* workspace = nullptr;
+    if (scratch)
+    {
+        if (need > scratch->bytes)
+            return fail(AWA_ERR_INVALID, std::string(p.split > 1 ? "key segments" : "text rows") +
+                                             " of this layer need " + std::to_string(need) +
+                                             " bytes, more than the no-alloc scratch buffer's " +
+                                             std::to_string(scratch->bytes));
+        workspace = scratch->ptr;
+    }
+    else
+    {
+        if ((rc = ensure_partials_locked(*plan, need)) != AWA_OK)
+            return rc;
+        workspace = plan->text_partials;
+    }
+    if (p.split > 1)
+    {
+        p.split_o = static_cast<float*>(workspace);
+        p.split_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + split_o_bytes(*plan, vl.heads, p.split));
+    }
+    else
+        p.text_partials = workspace;
     p.heads = vl.heads;
     p.text_tokens = plan->text_tokens;
     p.source_h = plan->source_h;
@@ -835,7 +971,30 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
     HIP_TRY(launch_attention_for(compute, p, stream), "attention kernel launch");
     if (after_attention)
         HIP_TRY(hipEventRecord(after_attention, stream), "hipEventRecord");
-    HIP_TRY(awa::launch_text_mean(partials, p.text_partial_elemsize, static_cast<int>(plan->windows.size()),
+    if (p.split > 1)
+    {
+        awa::SplitMerge m{};
+        m.o = p.split_o;
+        m.ml = p.split_ml;
+        m.split = p.split;
+        m.heads = vl.heads;
+        m.fused = true;
+        m.video_tokens = plan->source_tokens;
+        m.video_positions = plan->dev.video_positions;
+        m.source_h = plan->source_h;
+        m.source_w = plan->source_w;
+        m.video_out = sink;
+        m.text_tokens = plan->text_tokens;
+        m.window_count = static_cast<int>(plan->windows.size());
+        m.windows = plan->dev.windows;
+        m.text_out = text_out->data;
+        m.text_row = text_out->cstep;
+        m.text_elemsize = static_cast<int>(text_out->elemsize);
+        m.text_round_bf16 = text_out->elemsize == 2;
+        HIP_TRY(awa::launch_split_merge(m, stream), "split merge kernel launch");
+        return AWA_OK;
+    }
+    HIP_TRY(awa::launch_text_mean(workspace, p.text_partial_elemsize, static_cast<int>(plan->windows.size()),
                                   plan->text_tokens,
                                   vl.heads, vl.head_dim, text_out->data, text_out->cstep, text_out->elemsize, stream),
             "text mean kernel launch");
@@ -944,8 +1103,8 @@ int awa_window_attention(const awa_plan* plan, const awa_blob* input, const awa_
     const int align_elems = 16 / input->elemsize;
     if (!aligned16(input->data) || input->cstep % align_elems || !aligned16(output->data) || output->cstep % 4)
         return fail(AWA_ERR_INVALID, "packed blobs must be 16-byte aligned with 16-byte aligned strides");
-    std::lock_guard<std::mutex> lock(plan->mutex); // until the launch reads the work list
-    if ((rc = ensure_workspace_locked(*plan, heads, 0)) != AWA_OK)
+    std::lock_guard<std::mutex> lock(plan->mutex); // until the launches read the work list
+    if ((rc = ensure_work_locked(*plan, heads)) != AWA_OK)
         return rc;
     awa::AttentionLaunch p{};
     p.fused = false;
@@ -966,7 +1125,29 @@ int awa_window_attention(const awa_plan* plan, const awa_blob* input, const awa_
     p.source_h = plan->source_h;
     p.source_w = plan->source_w;
     p.scale_log2 = (1.f / std::sqrt(static_cast<float>(head_dim))) * 1.4426950408889634f;
+    if (p.split > 1)
+    {
+        // Key segments in the plan's workspace, combined into the packed rows.
+        if ((rc = ensure_partials_locked(*plan, split_bytes(*plan, heads, p.split))) != AWA_OK)
+            return rc;
+        p.split_o = plan->text_partials;
+        p.split_ml = reinterpret_cast<float2*>(reinterpret_cast<char*>(plan->text_partials) +
+                                               split_o_bytes(*plan, heads, p.split));
+    }
     HIP_TRY(launch_attention_for(compute, p, s), "attention kernel launch");
+    if (p.split > 1)
+    {
+        awa::SplitMerge m{};
+        m.o = p.split_o;
+        m.ml = p.split_ml;
+        m.split = p.split;
+        m.heads = heads;
+        m.fused = false;
+        m.sequence_tokens = plan->sequence_tokens;
+        m.packed_out = p.packed_out;
+        m.packed_row = p.packed_out_row;
+        HIP_TRY(awa::launch_split_merge(m, s), "split merge kernel launch");
+    }
     return AWA_OK;
 }
 

@@ -74,7 +74,47 @@ struct AttentionLaunch
     int text_tokens;
     int source_h, source_w;
     float scale_log2; // (1/sqrt(head_dim)) * log2(e)
+    // split > 1: every row's keys are split into `split` segments (the work
+    // items' key ranges); the kernel writes each segment's unnormalised row
+    // split_o[((p * heads + head) * split + seg) * head_dim + f] (p the packed
+    // row: window seq_start + window row) and its (running maximum in log2
+    // units, probability sum) to split_ml[same index / head_dim], and
+    // launch_split_merge combines them.
+    int split;
+    float* split_o;
+    float2* split_ml;
 };
+
+// Combines the key segments of a split layer (AttentionLaunch::split): per
+// row and head, M = max m_s, out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
+// Fused mode writes video rows to their grid position and the text rows'
+// window-order mean (each window's row rounded to bf16 first when
+// text_round_bf16, as the unsplit path's partials are); packed mode writes
+// every packed row to packed_out.
+struct SplitMerge
+{
+    const float* o;
+    const float2* ml;
+    int split, heads;
+    bool fused;
+    // fused: video
+    int video_tokens;
+    const int* video_positions; // token -> packed row
+    int source_h, source_w;
+    VideoSink video_out;
+    // fused: text
+    int text_tokens, window_count;
+    const WindowDesc* windows;
+    void* text_out;
+    long long text_row;
+    int text_elemsize;
+    bool text_round_bf16;
+    // packed
+    int sequence_tokens;
+    float* packed_out;
+    long long packed_row;
+};
+hipError_t launch_split_merge(const SplitMerge& m, hipStream_t stream);
 
 hipError_t launch_attention(const AttentionLaunch& p, hipStream_t stream);
 // LDS of one workgroup of that kernel: the static K/V tiles of the variant

@@ -207,6 +207,151 @@ __global__ void text_mean_kernel(const TPart* partials, int window_count, int te
             f32_to_bf16(sx / n) | (static_cast<uint32_t>(f32_to_bf16(sy / n)) << 16);
 }
 
+// ---- Split layers: the key segments of each row combined. Segment s of a
+// row holds O_s (unnormalised, relative to its running maximum m_s, in log2
+// units) and its probability sum l_s; with M = max m_s and w_s = 2^(m_s - M),
+// the row is (sum_s w_s O_s) * (1 / sum_s w_s l_s), the form the unsplit
+// kernels use (O * (1 / l)). ----
+template <int NB>
+__device__ __forceinline__ void merge_segments(const SplitMerge& m, const long long (&p)[NB], int head, int f0,
+                                               float (&r)[NB][8])
+{
+    // Rows p[0..NB) at once: every (max, sum) load, then every row load,
+    // issued before any is used (kMaxSegments unrolled, predicated by split).
+    constexpr int kMaxSegments = 8;
+    float2 ml[NB][kMaxSegments];
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int s = 0; s < kMaxSegments; s++)
+            if (s < m.split)
+                ml[j][s] = m.ml[(p[j] * m.heads + head) * m.split + s];
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+    {
+        const long long base = (p[j] * m.heads + head) * m.split;
+        float4 o[kMaxSegments][2];
+#pragma unroll
+        for (int s = 0; s < kMaxSegments; s++)
+            if (s < m.split)
+            {
+                const float4* src = reinterpret_cast<const float4*>(m.o + (base + s) * 128 + f0);
+                o[s][0] = src[0];
+                o[s][1] = src[1];
+            }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < kMaxSegments; s++)
+            if (s < m.split)
+                mx = fmaxf(mx, ml[j][s].x);
+        float l = 0.f;
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < kMaxSegments; s++)
+            if (s < m.split)
+            {
+                const float w = __builtin_amdgcn_exp2f(ml[j][s].x - mx);
+                l = fmaf(w, ml[j][s].y, l);
+                const float v[8] = {o[s][0].x, o[s][0].y, o[s][0].z, o[s][0].w,
+                                    o[s][1].x, o[s][1].y, o[s][1].z, o[s][1].w};
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    acc[i] = fmaf(w, v[i], acc[i]);
+            }
+        const float inv = 1.f / l;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            r[j][i] = acc[i] * inv;
+    }
+}
+
+__device__ __forceinline__ void store8(void* dst, int elemsize, const float (&r)[8])
+{
+    if (elemsize == 4)
+    {
+        float4* d = static_cast<float4*>(dst);
+        d[0] = make_float4(r[0], r[1], r[2], r[3]);
+        d[1] = make_float4(r[4], r[5], r[6], r[7]);
+    }
+    else
+    {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            w[i] = f32_to_bf16(r[2 * i]) | (static_cast<uint32_t>(f32_to_bf16(r[2 * i + 1])) << 16);
+        *static_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+// One thread per 8 features of one (row, head): fused mode covers the video
+// tokens, then the text rows (each a window-order mean); packed mode every
+// packed row.
+__global__ __launch_bounds__(kBlock) void split_merge_kernel(const SplitMerge m)
+{
+    const long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int f0 = 8 * static_cast<int>(idx & 15);
+    const long long row_head = idx >> 4;
+    const int head = static_cast<int>(row_head % m.heads);
+    const long long row = row_head / m.heads;
+    if (!m.fused)
+    {
+        if (row >= m.sequence_tokens)
+            return;
+        float r[1][8];
+        merge_segments<1>(m, {row}, head, f0, r);
+        store8(m.packed_out + row * m.packed_row + head * 128 + f0, 4, r[0]);
+        return;
+    }
+    if (row < m.video_tokens)
+    {
+        const int v = static_cast<int>(row);
+        float r[1][8];
+        merge_segments<1>(m, {static_cast<long long>(m.video_positions[v])}, head, f0, r);
+        const int area = m.source_h * m.source_w;
+        const int t = v / area;
+        const int h = (v - t * area) / m.source_w;
+        const int w = v - t * area - h * m.source_w;
+        const long long off = t * m.video_out.ts + h * m.video_out.hs + w * m.video_out.ws + head * 128 + f0;
+        store8(static_cast<unsigned char*>(m.video_out.data) + off * m.video_out.elemsize, m.video_out.elemsize,
+               r[0]);
+        return;
+    }
+    const int k = static_cast<int>(row - m.video_tokens);
+    if (k >= m.text_tokens)
+        return;
+    // Window-order sum of the windows' rows (rounded to bf16 first when the
+    // unsplit path would store bf16 partials), then the division by nwin;
+    // kBatch windows' loads at a time (indices past the last window are
+    // clamped to it and their rows not added).
+    constexpr int kBatch = 4;
+    float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int w0 = 0; w0 < m.window_count; w0 += kBatch)
+    {
+        long long pos[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; j++)
+        {
+            const WindowDesc win = m.windows[min(w0 + j, m.window_count - 1)];
+            pos[j] = win.seq_start + win.video_tokens + k;
+        }
+        float r[kBatch][8];
+        merge_segments<kBatch>(m, pos, head, f0, r);
+#pragma unroll
+        for (int j = 0; j < kBatch; j++)
+            if (w0 + j < m.window_count)
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    sum[i] += m.text_round_bf16 ? bf16_to_f32(f32_to_bf16(r[j][i])) : r[j][i];
+    }
+    const float n = static_cast<float>(m.window_count);
+    float r[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        r[i] = sum[i] / n;
+    store8(static_cast<unsigned char*>(m.text_out) + (k * m.text_row + head * 128 + f0) * m.text_elemsize,
+           m.text_elemsize, r);
+}
+
 // ---- DitRMSNorm (src/dit/dit_precision.cpp:63-86, src/dit/shader/dit_rmsnorm.comp):
 // one 128-thread workgroup per (row, channel). Lane l sums x[i]^2 over i = l,
 // l + 128, ... (products and sums rounded separately, as the shader's
@@ -431,6 +576,16 @@ hipError_t launch_text_mean(const void* partials, int partial_elemsize, int wind
                            text_token_stride, out_elemsize);
     else
         return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_split_merge(const SplitMerge& m, hipStream_t stream)
+{
+    if (m.split < 2 || m.heads <= 0)
+        return hipErrorInvalidValue;
+    const long long rows = m.fused ? static_cast<long long>(m.video_tokens) + m.text_tokens : m.sequence_tokens;
+    const long long total = rows * m.heads * 16;
+    hipLaunchKernelGGL(split_merge_kernel, dim3(grid_for(total)), dim3(kBlock), 0, stream, m);
     return hipGetLastError();
 }
 

@@ -30,9 +30,11 @@ struct alignas(16) WindowDesc
 
 // One workgroup's share of the fused / packed attention: the window (its
 // descriptor is embedded so that a workgroup needs a single dependent load to
-// start), the head and the query rows [row0, row0 + rows) of the window,
-// rows a multiple of 32 and at most the variant's rows per workgroup.
-// window < 0 marks padding.
+// start), the head, the query rows [row0, row0 + rows) of the window (rows a
+// multiple of 32 and at most the variant's rows per workgroup) and the keys
+// [key0, key1) of the window it attends to (key0 a multiple of 64): all L
+// keys, or, when a layer's units are split over several workgroups, segment
+// seg of them. window < 0 marks padding.
 struct alignas(16) WorkItem
 {
     WindowDesc win;
@@ -40,6 +42,9 @@ struct alignas(16) WorkItem
     int head;
     int row0;
     int rows;
+    int key0, key1;
+    int seg;
+    int pad;
 };
 
 // Packed-row descriptor for the staged kernels: source row (video index, or
@@ -101,6 +106,13 @@ struct awa_plan
     mutable int work_count = 0;
     mutable awa::WorkItem* work_wide = nullptr; // query blocks of kWideQueryRows rows
     mutable int work_wide_count = 0;
+    // The same query blocks with their keys split into segments (split_factor
+    // > 1; null otherwise), for layers whose units cannot fill the device.
+    mutable int split = 1, split_wide = 1;
+    mutable awa::WorkItem* work_split = nullptr;
+    mutable int work_split_count = 0;
+    mutable awa::WorkItem* work_wide_split = nullptr;
+    mutable int work_wide_split_count = 0;
     mutable float* text_partials = nullptr;
     mutable size_t text_partials_bytes = 0;
 };
