@@ -263,11 +263,9 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
             {
                 if constexpr (NORM)
                 {
-                    float ss = 0.f;
-#pragma unroll
-                    for (int e = 0; e < 8; e++)
-                        ss = fmaf(kv[e], kv[e], ss);
-                    const float coef = __builtin_amdgcn_rsqf(sum16(ss) * (1.f / kHeadDim) + p.norm_eps);
+                    // DitRMSNorm of the K row, bit for bit (its 16 chunks sit
+                    // in 16 consecutive lanes).
+                    const float coef = rms_coef_row16(kv, p.norm_eps);
                     const bool text = tile * KT + row >= win.video_tokens;
                     const float* const g = norm_lds + (text ? kHeadDim : 0) + 8 * kc;
                     const float4 g0 = *reinterpret_cast<const float4*>(g);
@@ -353,11 +351,27 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
         raw_to_float8<TIn>(qraw + c * kRW, qv + 8 * c);
     if constexpr (NORM)
     {
-        float ss = 0.f;
+        // DitRMSNorm of the Q row, bit for bit (rms_coef_row16's tree): qv[16c
+        // + i] holds feature 32c + 16*half + i, so strides 64 and 32 pair
+        // values of the lane, stride 16 the lane and its partner lane ^ 32,
+        // strides 8 to 1 values of the lane again.
+        float coef;
+        {
+#pragma clang fp contract(off)
+            float a[32];
 #pragma unroll
-        for (int e = 0; e < 64; e++)
-            ss = fmaf(qv[e], qv[e], ss);
-        const float coef = __builtin_amdgcn_rsqf(sum_xor32(ss) * (1.f / kHeadDim) + p.norm_eps);
+            for (int i = 0; i < 32; i++)
+                a[i] = qv[i] * qv[i] + qv[32 + i] * qv[32 + i];
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                a[i] = sum_xor32(a[i] + a[16 + i]);
+#pragma unroll
+            for (int w = 8; w > 0; w /= 2)
+#pragma unroll
+                for (int i = 0; i < w; i++)
+                    a[i] = a[i] + a[i + w];
+            coef = rms_coef(a[0], p.norm_eps);
+        }
         const float* const gamma = q_row >= win.video_tokens ? p.norm_gamma[2] : p.norm_gamma[0];
 #pragma unroll
         for (int c = 0; c < 4; c++)
@@ -428,7 +442,8 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
     const int vt_lane = (8 * half + ((lane & 15) >> 2)) * kXVPitch + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
     // Per-wave work on the tile in buffer buf: (a) the score classes 5 and 4,
-    // (b) classes 3 and 2, both combined into f; (c) softmax, P and PV.
+    // (b) classes 3 and 2: f = C3 + C4 / 2^8 + C5 / 2^16 (fp32, from the
+    // smallest up) and c2 = C2 (exact in fp32); (c) softmax, P and PV.
     auto scores_hi = [&](int buf, f32x16& f) {
         const unsigned char* const kb = k_lds + buf * kKBuf + col * kXKPitch + 16 * half;
         // ---- scores: S^T = K Q^T, four exact int32 classes ----
@@ -454,7 +469,7 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
                 f[i] = fmaf(static_cast<float>(c5[i]), 1.f / 256.f, static_cast<float>(c4[i]));
         }
     };
-    auto scores_lo = [&](int buf, f32x16& f) {
+    auto scores_lo = [&](int buf, f32x16& f, f32x16& c2f) {
         const unsigned char* const kb = k_lds + buf * kKBuf + col * kXKPitch + 16 * half;
         {
             i32x16 c3 = izero, c2 = izero;
@@ -471,11 +486,11 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
             for (int i = 0; i < 16; i++)
             {
                 f[i] = fmaf(f[i], 1.f / 256.f, static_cast<float>(c3[i]));
-                f[i] = fmaf(f[i], 1.f / 256.f, static_cast<float>(c2[i]));
+                c2f[i] = static_cast<float>(c2[i]);
             }
         }
     };
-    auto softmax_pv = [&](int tile, int buf, const f32x16& f, bool last) {
+    auto softmax_pv = [&](int tile, int buf, const f32x16& f, const f32x16& c2f, bool last) {
         // Register i holds key 16*(i/8) + 8*half + i%8 (key-permuted K rows).
         float kq[16];
         {
@@ -486,19 +501,21 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
             for (int i = 0; i < 16; i++)
                 kq[i] = kv[i] * qscale;
         }
-        float s[16];
-#pragma unroll
-        for (int i = 0; i < 16; i++)
-            s[i] = fmaf(f[i], kq[i], -row_max);
-        if (last && (L % KT))
-        {
-            const int key0 = tile * KT + 8 * half;
+        // Log2-domain score relative to the running maximum: (C2 + f / 2^8) kq
+        // - row_max as C2 kq - row_max (one rounding, near zero for the keys
+        // that matter) plus f kq / 2^8. Rounding the whole score first would
+        // cost an error of 2^-24 |score| (1e-4 of a probability at scores of
+        // ~1000, large shared Q/K directions) before the maximum cancels.
+        auto relative_scores = [&](float (&s)[16]) {
 #pragma unroll
             for (int i = 0; i < 16; i++)
-                if (key0 + 16 * (i >> 3) + (i & 7) >= L)
-                    s[i] = -INFINITY;
-        }
-        // ---- online softmax, relative to the running maximum ----
+                s[i] = fmaf(f[i], kq[i] * (1.f / 256.f), fmaf(c2f[i], kq[i], -row_max));
+        };
+        float s[16];
+        relative_scores(s);
+        // ---- online softmax, relative to the running maximum (keys past the
+        // window in a ragged last tile repeat its last key, so they leave the
+        // maximum unchanged and are masked below) ----
         float tile_max = s[0];
 #pragma unroll
         for (int i = 1; i < 16; i++)
@@ -506,10 +523,14 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
         tile_max = max_xor32(tile_max);
         if (tile == t_begin || __any(tile_max > kRescaleThreshold))
         {
-            const float delta = tile == t_begin ? tile_max : fmaxf(tile_max, 0.f);
+            // New maximum; the old terms are rescaled by 2^(old - new), the
+            // exact difference of the two maxima, and the scores recomputed
+            // relative to the new one (not shifted, which would round them at
+            // their full magnitude).
+            const float new_max = row_max + (tile == t_begin ? tile_max : fmaxf(tile_max, 0.f));
             if (tile != t_begin)
             {
-                const float alpha = __builtin_amdgcn_exp2f(-delta);
+                const float alpha = __builtin_amdgcn_exp2f(row_max - new_max);
                 row_sum *= alpha;
 #pragma unroll
                 for (int db = 0; db < 4; db++)
@@ -517,10 +538,16 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
                     for (int i = 0; i < 16; i++)
                         o[db][i] *= alpha;
             }
-            row_max += delta;
+            row_max = new_max;
+            relative_scores(s);
+        }
+        if (last && (L % KT))
+        {
+            const int key0 = tile * KT + 8 * half;
 #pragma unroll
             for (int i = 0; i < 16; i++)
-                s[i] -= delta;
+                if (key0 + 16 * (i >> 3) + (i & 7) >= L)
+                    s[i] = -INFINITY;
         }
         // ---- P = p1 + p2 + p3 as bf16 operands (p1, p2 truncations, p3 the
         // rounded rest: all of p's 24 bits); the row sum adds the fp32 P ----
@@ -613,9 +640,10 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
             if (wave_active)
             {
                 f32x16 f;
+                f32x16 c2f;
                 scores_hi(buf, f);
-                scores_lo(buf, f);
-                softmax_pv(tile, buf, f, tile == tiles - 1);
+                scores_lo(buf, f, c2f);
+                softmax_pv(tile, buf, f, c2f, tile == tiles - 1);
             }
             if (!stage_first)
                 stage();
@@ -635,9 +663,10 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
             if (wave_active)
             {
                 f32x16 f;
+                f32x16 c2f;
                 scores_hi(0, f);
-                scores_lo(0, f);
-                softmax_pv(tile, 0, f, tile == tiles - 1);
+                scores_lo(0, f, c2f);
+                softmax_pv(tile, 0, f, c2f, tile == tiles - 1);
             }
             __syncthreads();
         }

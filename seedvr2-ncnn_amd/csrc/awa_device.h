@@ -242,6 +242,50 @@ __device__ __forceinline__ float sum_xor32(float x)
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Row x of DitRMSNorm over 128 features (src/dit/shader/dit_rmsnorm.comp,
+// src/dit/dit_precision.cpp:63-86) reproduced bit for bit: the shader's 128
+// lanes each hold one square, which a tree adds at strides 64, 32, ..., 1
+// (lane i += lane i + stride); then 1 / sqrt(sum / 128 + eps), correctly
+// rounded. These helpers pair the same values (fp addition commutes, so the
+// order within a pair does not matter) for the feature layouts the kernels
+// hold, without contraction.
+__device__ __forceinline__ float rms_coef(float sum, float eps)
+{
+#pragma clang fp contract(off)
+    return 1.f / sqrtf(sum * (1.f / 128.f) + eps);
+}
+
+// 16 consecutive lanes hold a row, lane j (of the 16) features 8j + [0, 8).
+// Strides 64, 32, 16, 8 pair lane j with lane j + 8, 4, 2, 1 (mod 16; DPP row
+// rotations), strides 4, 2, 1 the lane's own values. Every lane of the 16
+// returns the coefficient.
+__device__ __forceinline__ float rms_coef_row16(const float (&x)[8], float eps)
+{
+#pragma clang fp contract(off)
+    float a[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+        a[e] = x[e] * x[e];
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+        a[e] = a[e] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a[e]), 0x128, 0xF, 0xF, false));
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+        a[e] = a[e] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a[e]), 0x124, 0xF, 0xF, false));
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+        a[e] = a[e] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a[e]), 0x122, 0xF, 0xF, false));
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+        a[e] = a[e] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a[e]), 0x121, 0xF, 0xF, false));
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        a[e] = a[e] + a[e + 4];
+    a[0] = a[0] + a[2];
+    a[1] = a[1] + a[3];
+    return rms_coef(a[0] + a[1], eps);
+}
+
 // Bytes of the dynamic-LDS K gammas of the fused q/k RMSNorm (video, text).
 template <bool NORM>
 constexpr int kNormLdsBytes = NORM ? 2 * kHeadDim * 4 : 0;

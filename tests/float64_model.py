@@ -81,3 +81,23 @@ def layer64(g: O.Geometry, video: np.ndarray, text: np.ndarray, mistake: str | N
         vid[idx] = o[:len(idx)]
         txt += o[len(idx):]
     return vid, txt / len(windows)
+
+
+def layer64_of_rotated(g: O.Geometry, video: np.ndarray, text: np.ndarray):
+    """The layer in float64 after the reference's fp32 Pack and MMRoPE (the
+    oracle's): Q and K carry the fp32 rotation's rounding, everything after
+    it is exact. Its distance to a result measures that result's attention
+    arithmetic alone (the fp32 rotation, which every fp32 implementation of
+    the reference's data flow shares, cancels)."""
+    heads, d = video.shape[2], video.shape[3]
+    m = O.build_maps(g)
+    packed, _ = O.pack_forward(g, video, text, heads, d)
+    roped = O.mmrope_forward(packed, O.rope_table(g), heads, d).reshape(m.sequence_tokens, 3, heads, d)
+    out = np.zeros((m.sequence_tokens, heads, d))
+    cu = m.cu_seqlens
+    for w in range(m.window_count):
+        a, b = cu[w], cu[w + 1]
+        out[a:b] = attention64(roped[a:b, 0], roped[a:b, 1], roped[a:b, 2])
+    vid = out[m.video_positions]
+    txt = out[m.text_positions.reshape(m.window_count, g.text_tokens)].mean(axis=0)
+    return vid, txt

@@ -20,12 +20,19 @@ so is an exactly rounded fp32 computation. The gate is therefore:
 
 - max abs error against the oracle <= 1e-4 wherever the oracle is itself
   within 4e-5 of float64 (two fifths of the budget);
-- everywhere, max abs error against float64 <= max(1e-4, 2 x the oracle's
-  own error against float64): as close to the exact result as the
+- everywhere, max abs error against float64 <= max(1e-4, 1.5 x the
+  oracle's own error against float64): as close to the exact result as the
   reference's GPU arithmetic, up to the spread of a maximum over rounding
-  errors (exactly rounded scores reach 1.65 x);
+  errors (the fused q/k RMSNorm reproduces DitRMSNorm bit for bit, so the
+  norm scenarios see the oracle's Q and K);
 - everywhere, no further from float64 than the reference's CPU arithmetic
-  where that is beyond the budget.
+  where that is beyond the budget;
+- the attention arithmetic alone (against the float64 layer of the
+  fp32-rotated Q/K, which removes the rounding of the fp32 MMRoPE that every
+  fp32 implementation of the reference's data flow shares) no further from
+  exact than the oracle's, or within 1e-5: the kernel rounds each score once,
+  relative to the running maximum, where the reference rounds it at its full
+  magnitude.
 """
 
 from __future__ import annotations
@@ -37,7 +44,7 @@ import awa_hip as A
 import oracle as O
 from awa_cases import CONFIGS, HEAD_DIM, abs_err, geometry, qkv_inputs
 from device_blobs import mat3, qkv_blob, read_mat3, read_video, video_out_blob
-from float64_model import layer64
+from float64_model import layer64, layer64_of_rotated
 
 pytestmark = pytest.mark.gpu
 
@@ -110,20 +117,27 @@ def test_fp32_large_magnitudes(gpu, name, shifted):
         ref_v, ref_t = O.awa_layer(g, video, text, HEADS, HEAD_DIM)
         cpu_v, cpu_t = O.awa_layer(g, video, text, HEADS, HEAD_DIM, attention_order="cpu", text_order="cpu")
         ex_v, ex_t = layer64(g, video, text)
+        ar_v, ar_t = layer64_of_rotated(g, video, text)
         got = np.concatenate([got_v.ravel(), got_t.ravel()])
         ref = np.concatenate([ref_v.ravel(), ref_t.ravel()])
         cpu = np.concatenate([cpu_v.ravel(), cpu_t.ravel()])
         ex = np.concatenate([ex_v.ravel(), ex_t.ravel()])
+        ar = np.concatenate([ar_v.ravel(), ar_t.ravel()])
+        # Attention arithmetic alone: against the exact layer of the fp32-rotated Q/K.
+        arith, arith_oracle = abs_err(got, ar), abs_err(ref, ar)
         e_oracle = abs_err(got, ref)
         e_exact = abs_err(got, ex)
         oracle_exact = abs_err(ref, ex)
         cpu_exact = abs_err(cpu, ex)
         print(f"  {scen:14s} vs oracle {e_oracle:.2e}  vs float64 {e_exact:.2e}  oracle vs float64 {oracle_exact:.2e}"
-              f"  cpu-order oracle vs float64 {cpu_exact:.2e}", flush=True)
+              f"  cpu-order oracle vs float64 {cpu_exact:.2e}  attention arithmetic: kernel {arith:.2e}"
+              f" oracle {arith_oracle:.2e}", flush=True)
         if oracle_exact <= ORACLE_ACCURATE and e_oracle > FP32_ATOL:
             failures.append((scen, "oracle", e_oracle))
-        if e_exact > max(FP32_ATOL, 2.0 * oracle_exact):
+        if e_exact > max(FP32_ATOL, 1.5 * oracle_exact):
             failures.append((scen, "float64", e_exact, oracle_exact))
         if e_exact > max(FP32_ATOL, cpu_exact):
             failures.append((scen, "cpu-order", e_exact, cpu_exact))
+        if arith > max(1e-5, arith_oracle):
+            failures.append((scen, "attention arithmetic", arith, arith_oracle))
     assert not failures, failures

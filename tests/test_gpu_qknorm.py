@@ -126,15 +126,22 @@ def test_fused_qknorm_bf16(gpu, in_elem, out_elem):
     assert rel_err(got_t, ref_t) <= 2e-2
 
 
-def test_fused_qknorm_matches_unfused_chain(gpu):
-    """Fused prologue == standalone norm of Q and K into an fp32 QKV, then
-    awa_forward (the reference's DitRMSNorm -> DitQKVConcat -> AWA data flow),
-    to the few-ulp difference of the two norm arithmetics."""
-    g = geometry(CONFIGS["image_1x16x16"], False)
-    print("case qknorm fused vs unfused", flush=True)
+@pytest.mark.parametrize("name,shifted,scale", [("image_1x16x16", False, 1.0), ("clip_9x16x16", True, 3.0),
+                                               ("clip_9x16x16", False, 8.0)])
+def test_fused_qknorm_matches_unfused_chain(gpu, name, shifted, scale):
+    """fp32: the fused prologue gives the bits of the standalone norm of Q and
+    K into an fp32 QKV followed by awa_forward (the reference's DitRMSNorm ->
+    DitQKVConcat -> AWA data flow): the fused norm reproduces DitRMSNorm's
+    tree-ordered sum and correctly rounded coefficient exactly, on raw
+    projections of unit scale and scaled by 3 and 8 (gammas up to 20)."""
+    g = geometry(CONFIGS[name], shifted)
+    print(f"case qknorm fused vs unfused {name} shifted={shifted} scale={scale}", flush=True)
     heads = 4
     video, text = qkv_inputs(g, heads, HEAD_DIM, 5150)
-    gammas = gamma_set(11)
+    video[:, :2] *= scale
+    text[:, :2] *= scale
+    gammas = gamma_set(11) if scale == 1.0 else [
+        np.random.RandomState(int(scale)).uniform(0.0, 20.0, HEAD_DIM).astype(np.float32) for _ in range(4)]
     fused_v, fused_t = run_fused_qknorm(g, video, text, gammas, A.COMPUTE_F32)
     # Unfused: layout 'b' keeps Q, K and V as three contiguous [T][H][d] blocks.
     dg = DeviceGammas(gammas)
@@ -158,8 +165,8 @@ def test_fused_qknorm_matches_unfused_chain(gpu):
     A.synchronize()
     un_v = read_video(vo, g.t, g.h, g.w, heads, HEAD_DIM)
     un_t = read_mat3(to)
-    assert abs_err(fused_v, un_v) <= 2e-5
-    assert abs_err(fused_t, un_t) <= 2e-5
+    np.testing.assert_array_equal(fused_v, un_v)
+    np.testing.assert_array_equal(fused_t, un_t)
 
 
 def test_qknorm_invalid_arguments(gpu):
