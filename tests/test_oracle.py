@@ -22,7 +22,7 @@ import pytest
 
 import oracle as O
 from awa_cases import CONFIGS, RAGGED
-from float64_model import attention64, layer64, rope_apply64, rope_frequencies64
+from float64_model import attention64, layer64, layer64_of_rotated, rope_apply64, rope_frequencies64
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
@@ -310,6 +310,28 @@ def test_layer_matches_float64_definition(name, shifted):
         v, t = O.awa_layer(g, video, text, heads, d, attention_order=order, text_order=text_order)
         assert np.max(np.abs(v - ref_v)) < 1e-5
         assert np.max(np.abs(t - ref_t)) < 1e-5
+
+
+@pytest.mark.parametrize("name,shifted", [("clip_2x16x16", True), ("image_1x16x16", False)])
+def test_layer_of_rotated_inputs(name, shifted):
+    """The float64 layer after the fp32 rotation (the large-magnitude tests'
+    attention-arithmetic reference) is the float64 layer up to that
+    rotation's rounding (a few 1e-7 at unit scale), and the Kahan-order
+    oracle, which rotates identically, is closer to it than to the fully
+    float64 layer."""
+    g = geometry(name, shifted)
+    heads, d = 2, 128
+    rng = np.random.default_rng(23)
+    video = rng.standard_normal((g.source_tokens, 3, heads, d)).astype(np.float32)
+    text = rng.standard_normal((g.text_tokens, 3, heads, d)).astype(np.float32)
+    rv, rt = layer64_of_rotated(g, video, text)
+    ev, et = layer64(g, video, text)
+    assert np.max(np.abs(rv - ev)) < 2e-6 and np.max(np.abs(rt - et)) < 2e-6
+    ov, ot = O.awa_layer(g, video, text, heads, d)
+    assert np.max(np.abs(ov - rv)) < np.max(np.abs(ov - ev)) and np.max(np.abs(ov - rv)) < 1e-6
+    # A planted mistake (text rows summed over windows, not averaged) is caught.
+    m = O.build_maps(g)
+    assert np.max(np.abs(rt * m.window_count - et)) > 1e-2
 
 
 @pytest.mark.parametrize("mistake", ["sin_sign", "pair_swap", "text_offset", "no_scale"])
