@@ -44,6 +44,10 @@ FP32_PREFIX = 9
 PEAK_BF16 = 2.5e15
 PEAK_FP32 = 157.3e12
 PEAK_HBM = 8.0e12
+# MI355X peak engine clock and SIMDs (256 CUs x 4): the MFMA instruction roof
+# of a kernel is its MFMA cycles spread evenly over the SIMDs at this clock.
+PEAK_CLOCK_HZ = 2.4e9
+SIMDS = 1024
 
 
 def cpu_baseline(sample_layers: int) -> dict:
@@ -195,6 +199,25 @@ CONFIGS = {
     "bf16_production_256": ((1, 16, 16), (4, 3, 3), "bf16", ("unshifted",)),
 }
 MALL_BYTES = 256 * 1024 * 1024
+
+
+def mfma_instruction_roof_ms(A, grid, windows, shifted: bool, label: str) -> float:
+    """Time the layer's attention kernel needs for its MFMA instructions
+    alone, at the peak clock with every SIMD busy. Each 32-row wave of a
+    (window, head) unit covers all of the unit's keys; a 32x32x16 bf16 and a
+    32x32x32 int8 MFMA each keep a SIMD busy 32 cycles. bf16 kernel: 32 MFMAs
+    per wave and 64-key tile (16 for S^T = K Q^T, 16 for O^T += V^T P^T).
+    Exact-score fp32 kernel: 88 per wave and 32-key tile (40 int8 for the
+    score classes, 48 bf16 for the three-piece PV)."""
+    plan = A.Plan(A.LayerParams(*grid, *windows, TEXT, shifted))
+    wins = plan.windows()
+    plan.destroy()
+    mfmas = 0
+    for t0, t1, h0, h1, w0, w1 in wins:
+        L = (t1 - t0) * (h1 - h0) * (w1 - w0) + TEXT
+        waves = -(-L // 32)
+        mfmas += waves * (-(-L // 64) * 32 if label == "bf16" else -(-L // 32) * 88)
+    return mfmas * HEADS * 32 / SIMDS / PEAK_CLOCK_HZ * 1e3
 
 
 def key_segments(A, grid, windows, shifted: bool, label: str) -> int:
@@ -524,8 +547,15 @@ def main() -> int:
 
     even = lambda idx: idx[idx % 2 == 0]
     odd = lambda idx: idx[idx % 2 == 1]
-    bf16_layers = {"unshifted": layer_stats(even(bf16_idx)), "shifted": layer_stats(odd(bf16_idx))}
-    fp32_layers = {"unshifted": layer_stats(even(fp32_idx)), "shifted": layer_stats(odd(fp32_idx))}
+    def with_roof(stats, label, shifted):
+        roof = mfma_instruction_roof_ms(A, GRID, WINDOWS, shifted, label)
+        return {**stats, "mfma_instruction_roof_ms": round(roof, 5),
+                "mfma_instruction_roof_frac": round(roof / stats["kernel_ms"], 4)}
+
+    bf16_layers = {"unshifted": with_roof(layer_stats(even(bf16_idx)), "bf16", False),
+                   "shifted": with_roof(layer_stats(odd(bf16_idx)), "bf16", True)}
+    fp32_layers = {"unshifted": with_roof(layer_stats(even(fp32_idx)), "fp32", False),
+                   "shifted": with_roof(layer_stats(odd(fp32_idx)), "fp32", True)}
     bf16_all_ms = float(att[bf16_idx].sum())
     bf16_pct = 100.0 * float(flops[bf16_idx].sum()) / (bf16_all_ms * 1e-3) / PEAK_BF16
 

@@ -188,9 +188,9 @@ int attention_variant(int compute, const awa_plan& plan)
     return idle_wide <= idle_narrow ? awa::kVariantWide : awa::kVariantNarrow;
 }
 
-// The variant to launch: attention_variant's choice, or, for the
-// exact-score fp32 kernel, its single-buffered 4-wave form when the
-// double-buffered 8-wave form's tiles and tables exceed a workgroup's LDS.
+// The variant to launch: attention_variant's choice, or the 4-wave form
+// (single-buffered, two workgroups per CU) when the double-buffered 8-wave
+// form's tiles and tables exceed a workgroup's LDS.
 // Returns -1 with the reason set when no variant fits the window.
 int launch_variant(int compute, const awa_plan& plan, awa::AttentionLaunch& p)
 {
@@ -212,7 +212,7 @@ int launch_variant(int compute, const awa_plan& plan, awa::AttentionLaunch& p)
     fused.fused = true;
     fused.qk_norm = true;
     fused.rope_coords = plan.rope_coords;
-    if (compute == AWA_COMPUTE_F32 && p.variant == awa::kVariantWide && lds(p.variant, fused) > awa::kWorkgroupLds)
+    if (p.variant == awa::kVariantWide && lds(p.variant, fused) > awa::kWorkgroupLds)
         p.variant = awa::kVariantNarrow;
     if (lds(p.variant, p) > awa::kWorkgroupLds)
         return fail(AWA_ERR_INVALID, "window of " + std::to_string(plan.max_window_tokens) +
