@@ -1,11 +1,12 @@
 // awa_forward_noalloc: the fused AWA layer without device allocation.
 //
 // The only device memory awa_forward allocates while it runs is the plan's
-// text-row workspace ([nwin][T_x][H][d] rows, averaged afterwards) and, on
-// the first call with a head count, the work list. Here the text rows go to
-// a file-scope device array, one copy per GPU, and the work list must
-// already be on the device (awa_plan_upload builds it when the plan desc
-// names the head count).
+// workspace (the per-window text rows [nwin][T_x][H][d], averaged
+// afterwards, or a split layer's key segments, combined afterwards) and, on
+// the first call with a head count, the work lists. Here the workspace is a
+// file-scope device array, one copy per GPU, and the work lists must already
+// be on the device (awa_plan_upload builds them when the plan desc names the
+// head count).
 //
 // In host code the array's name is only a host-side stand-in: its device
 // address on each GPU comes from hipGetSymbolAddress, taken once per device
