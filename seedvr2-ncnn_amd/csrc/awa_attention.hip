@@ -46,6 +46,7 @@ namespace
 using namespace dev;
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 // Bytes of one wave's output stage: 32 rows of 128 bf16 features and 32 row
@@ -886,7 +887,10 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
         // c ^ (i & 15): conflict-free both ways), then reads them back 16
         // bytes a lane, 16 lanes a row, and writes whole 256-byte rows. Rows
         // with an fp32 destination (fp32 outputs or text rows) are stored
-        // directly; rows past the window are not stored. ----
+        // directly; rows past the window are not stored. The row stores are
+        // nontemporal: dirty lines left in L2 lengthen the kernel's end (the
+        // text mean then reads its rows from beyond L2, which costs it less
+        // than the attention kernel gains). ----
         if (!wave_active)
             return;
         const float inv = 1.f / sum_xor32(row_sum);
@@ -939,10 +943,10 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
         for (int j = 0; j < 8; j++)
         {
             const int row = 4 * j + (lane >> 4);
-            const uint4 v = *reinterpret_cast<const uint4*>(rows_lds + row * kHeadDim + 8 * (chunk ^ (row & 15)));
+            const u32x4 v = *reinterpret_cast<const u32x4*>(rows_lds + row * kHeadDim + 8 * (chunk ^ (row & 15)));
             uint16_t* const d = reinterpret_cast<uint16_t*>(dst_lds[row]);
             if (d)
-                *reinterpret_cast<uint4*>(d + 8 * chunk) = v;
+                __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(d + 8 * chunk));
         }
         return;
     }
