@@ -50,6 +50,7 @@ using namespace dev;
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int kXKeys = 32;       // keys per tile
@@ -57,6 +58,8 @@ constexpr int kXKPitch = 144;    // bytes per key row of one int8 K slice (128 +
 constexpr int kXKSlice = kXKeys * kXKPitch;
 constexpr int kXVPitch = 160;    // bf16 elements per key row of one V slice (conflict-free transposed reads)
 constexpr int kXVSlice = kXKeys * kXVPitch * 2;
+// One wave's output stage: 8 fp32 rows of 512 bytes and their 8 destinations.
+constexpr int kXOutStageWaveBytes = 8 * 512 + 64;
 
 // x ~= 2^(e-6) (d1 + d2 2^-8 + d3 2^-16 + d4 2^-24) for |x| < 2^e: X = x *
 // 2^(30-e) truncated (|X| < 2^30) plus 128 (1 + 2^8 + 2^16), so that its top
@@ -687,6 +690,75 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
             p.split_ml[slot] = make_float2(row_max, l);
         return;
     }
+    if constexpr (FUSED && WIDE && sizeof(TOut) == 4)
+        if (p.text_partial_elemsize == 4)
+        {
+            // ---- 8-wave form: fp32 rows through LDS, 8 rows per pass (the V
+            // tiles' space, free after the loop's last barrier): the lane
+            // pair (col, half) holds row col's 16-byte chunks 8 db + 2 g +
+            // half, written at position chunk ^ (2 row) of the row
+            // (conflict-free), read back 16 bytes a lane, 32 lanes a row, and
+            // stored as whole 512-byte rows with nontemporal stores (dirty
+            // lines left in L2 lengthen the kernel's end; the text mean then
+            // reads its rows from beyond L2, which costs it less than the
+            // attention kernel gains). The 4-wave form measured slower this
+            // way and stores its rows directly. ----
+            if (!wave_active)
+                return;
+            const float inv = 1.f / sum_xor32(row_sum);
+            float* dst = nullptr;
+            if (q_valid)
+            {
+                const RowRef r = decode(qi);
+                dst = !r.text ? static_cast<float*>(p.video_out.data) + r.t * p.video_out.ts + r.h * p.video_out.hs +
+                                    r.w * p.video_out.ws + head_off
+                              : static_cast<float*>(p.text_partials) +
+                                    ((static_cast<long long>(item.window) * p.text_tokens + r.k) * p.heads + head) *
+                                        kHeadDim;
+            }
+            unsigned char* const region = v_lds + wave * kXOutStageWaveBytes;
+            float* const rows_lds = reinterpret_cast<float*>(region);
+            unsigned long long* const dst_lds = reinterpret_cast<unsigned long long*>(region + 8 * 512);
+            const int c = lane & 31;
+#pragma unroll
+            for (int pass = 0; pass < 4; pass++)
+            {
+                const int rl = col - 8 * pass;
+                if (rl >= 0 && rl < 8)
+                {
+#pragma unroll
+                    for (int db = 0; db < 4; db++)
+#pragma unroll
+                        for (int g = 0; g < 4; g++)
+                        {
+                            const int pos = (8 * db + 2 * g + half) ^ (2 * rl);
+                            *reinterpret_cast<f32x4*>(rows_lds + rl * kHeadDim + 4 * pos) =
+                                f32x4{o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv,
+                                      o[db][4 * g + 3] * inv};
+                        }
+                    if (half == 0)
+                        dst_lds[rl] = reinterpret_cast<unsigned long long>(dst);
+                }
+                // The wave reads what its own lanes wrote.
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                {
+                    const int row = 2 * i + (lane >> 5);
+                    const f32x4 v = *reinterpret_cast<const f32x4*>(rows_lds + row * kHeadDim + 4 * (c ^ (2 * row)));
+                    float* const d = reinterpret_cast<float*>(dst_lds[row]);
+                    if (d)
+                        __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(d + 4 * c));
+                }
+                // The next pass rewrites the region only after these reads.
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
+            return;
+        }
     if (!q_valid)
         return;
     const float inv = 1.f / sum_xor32(row_sum);
@@ -751,6 +823,9 @@ size_t attention_x_dynamic_lds(const AttentionLaunch& p, bool norm)
     const size_t row_table = static_cast<size_t>((p.max_window_tokens + 63) & ~63) * (2 * sizeof(long long) + 4);
     return (norm ? 2 * kHeadDim * 4 : 0) + dev::rope_table_bytes(p.fused, p.rope_coords) + row_table;
 }
+
+static_assert(4 * kXOutStageWaveBytes <= 3 * kXVSlice && 8 * kXOutStageWaveBytes <= 2 * 3 * kXVSlice,
+              "the output stage fits the V tiles");
 
 size_t attention_x_static_lds(bool wide)
 {
