@@ -282,14 +282,16 @@ int device_cus()
 // one 8-wave workgroup per CU) and every unit has at least kMinSplitTiles
 // 64-key tiles, the most segments (at most 8) that still fit those slots with
 // at least one tile per segment in every unit. The production 256x256 layer
-// (20 units of 320 rows) then uses the whole device. Shorter units, and the
-// bf16 kernel, whose items are dominated by their start-up, lose more to the
-// fp32 segment rows and the combining kernel than they gain (measured on the
-// 1x16x16 image, 2x16x16 clip and production layers). The environment
-// variable SEEDVR2_AWA_SPLIT=0, read when a plan builds its work lists, turns
-// splitting off.
+// (20 units of 320 rows) then uses the whole device (41 -> 31 us), and the
+// unshifted 2x16x16 clip (80 units of 192 rows) splits in three (37.5 -> 32.8
+// us). Units of 128 rows (the 1x16x16 image: 24.5 -> 25.6 us at two
+// segments), and the bf16 kernel, whose items are dominated by their start-up
+// and whose text mean reads half the bytes of the combining kernel (13.2 ->
+// 20.0 us on the bf16 image), lose more to the segment rows and the combining
+// kernel than they gain. The environment variable SEEDVR2_AWA_SPLIT=0, read
+// when a plan builds its work lists, turns splitting off.
 constexpr int kMaxSplit = 8;
-constexpr int kMinSplitTiles = 4;
+constexpr int kMinSplitTiles = 3;
 int split_factor(const awa_plan& plan, int heads, int rows_per_block)
 {
     const char* env = std::getenv("SEEDVR2_AWA_SPLIT");

@@ -54,6 +54,8 @@ def run_fused(g, video, text, compute, elem, split_on=True):
     ("production_256", False, A.COMPUTE_BF16, 20, 1),
     ("production_256", False, A.COMPUTE_F32_MFMA, 20, 1),
     ("image_1x16x16", False, A.COMPUTE_F32, 20, 1),
+    ("clip_2x16x16", False, A.COMPUTE_F32, 20, 3),
+    ("clip_2x16x16", True, A.COMPUTE_F32, 20, 1),
     ("clip_2x16x16", True, A.COMPUTE_BF16, 20, 1),
     ("clip_9x16x16", False, A.COMPUTE_F32, 20, 1),
     ("clip_9x16x16", True, A.COMPUTE_F32, 20, 1),
@@ -62,10 +64,11 @@ def run_fused(g, video, text, compute, elem, split_on=True):
 ])
 def test_split_factor(gpu, name, shifted, compute, heads, expect):
     """The production layer's 20 units of 320 rows split in five (one per
-    64-key tile) in fp32; bf16 and the pipelined fp32-MFMA variant never
-    split; units of under four 64-key tiles (image, shifted windows) do not;
-    the 33-frame layer fills the device unsplit at 20 heads and splits in
-    four (48 8-wave items) at 4."""
+    64-key tile) in fp32, the unshifted 2x16x16 clip's 80 units of 192 rows
+    in three; bf16 and the pipelined fp32-MFMA variant never split; units of
+    under three 64-key tiles (image, shifted windows) do not; the 33-frame
+    layer fills the device unsplit at 20 heads and splits in four (48 8-wave
+    items) at 4."""
     g = geometry(CONFIGS[name], shifted)
     plan = A.Plan(A.LayerParams(*g.args, g.text_tokens, g.shifted))
     plan.upload()
@@ -96,6 +99,7 @@ def test_production_layer_matches_oracle(gpu, compute):
 @pytest.mark.parametrize("name,shifted,heads,elem", [
     ("production_256", False, 20, 4),
     ("production_256", False, 20, 2),
+    ("clip_2x16x16", False, 20, 4),
     ("clip_9x16x16", False, 4, 4),
 ])
 def test_split_matches_unsplit(gpu, name, shifted, heads, elem):
