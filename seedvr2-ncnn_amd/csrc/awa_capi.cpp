@@ -937,13 +937,21 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
     p.max_window_tokens = plan->max_window_tokens;
     if ((rc = launch_variant(compute, *plan, p)) != AWA_OK)
         return rc;
+    // A single window's text rows are the text output itself (the mean of one
+    // row is that row): with a dense text output they are written there and
+    // the text-mean kernel is skipped.
+    const bool text_direct = p.split == 1 && plan->windows.size() == 1 &&
+                             text_out->cstep == static_cast<long long>(vl.heads) * vl.head_dim;
     // Workspace: the per-window text rows, or a split layer's key segments;
     // in the caller's scratch buffer (no allocation) or the plan's.
-    const size_t need = p.split > 1 ? split_bytes(*plan, vl.heads, p.split)
-                                    : plan->windows.size() * static_cast<size_t>(plan->text_tokens) * vl.heads *
-                                          vl.head_dim * static_cast<size_t>(text_out->elemsize);
+    const size_t need = text_direct ? 0
+                        : p.split > 1 ? split_bytes(*plan, vl.heads, p.split)
+                                      : plan->windows.size() * static_cast<size_t>(plan->text_tokens) * vl.heads *
+                                            vl.head_dim * static_cast<size_t>(text_out->elemsize);
     void* workspace = nullptr;
-    if (scratch)
+    if (text_direct)
+        workspace = text_out->data;
+    else if (scratch)
     {
         if (need > scratch->bytes)
             return fail(AWA_ERR_INVALID, std::string(p.split > 1 ? "key segments" : "text rows") +
@@ -996,6 +1004,8 @@ int forward_fused(const awa_plan* plan, const awa_blob* video_qkv, const awa_blo
         HIP_TRY(awa::launch_split_merge(m, stream), "split merge kernel launch");
         return AWA_OK;
     }
+    if (text_direct)
+        return AWA_OK;
     HIP_TRY(awa::launch_text_mean(workspace, p.text_partial_elemsize, static_cast<int>(plan->windows.size()),
                                   plan->text_tokens,
                                   vl.heads, vl.head_dim, text_out->data, text_out->cstep, text_out->elemsize, stream),

@@ -145,3 +145,50 @@ def test_staged_split_matches_fused(gpu):
     A.synchronize()
     np.testing.assert_array_equal(read_video(vo, g.t, g.h, g.w, heads, HEAD_DIM), fv)
     np.testing.assert_array_equal(read_mat3(to), ft)
+
+
+@pytest.mark.parametrize("compute,elem,split_on", [(A.COMPUTE_F32, 4, False), (A.COMPUTE_BF16, 2, True),
+                                                   (A.COMPUTE_BF16, 4, True)])
+def test_single_window_text_written_directly(gpu, compute, elem, split_on):
+    """A layer of one window (the production layer) writes its text rows
+    straight to the text output, the mean of one row being that row: against
+    the oracle, and in fp32 bit for bit against the staged chain, whose
+    Unpack takes the mean."""
+    g = geometry(CONFIGS["production_256"], False)
+    heads = 8
+    bf16 = compute == A.COMPUTE_BF16
+    print(f"case single window text direct bf16={bf16} out elem={elem}", flush=True)
+    video, text = qkv_inputs(g, heads, HEAD_DIM, 20260904)
+    if bf16:
+        video, text = bf16_round(video), bf16_round(text)
+    ref_v, ref_t = O.awa_layer(g, video, text, heads, HEAD_DIM)
+    fv, ft, split = run_fused(g, video, text, compute, elem, split_on=split_on)
+    assert split == 1
+    if bf16:
+        assert rel_err(fv, ref_v) <= 2e-2 and rel_err(ft, ref_t) <= 2e-2
+        return
+    assert abs_err(fv, ref_v) <= 1e-4 and abs_err(ft, ref_t) <= 1e-4
+    old = os.environ.pop("SEEDVR2_AWA_SPLIT", None)
+    os.environ["SEEDVR2_AWA_SPLIT"] = "0"
+    try:
+        plan = A.Plan(A.LayerParams(*g.args, g.text_tokens, g.shifted), heads=heads)
+        plan.upload()
+    finally:
+        os.environ.pop("SEEDVR2_AWA_SPLIT", None)
+        if old is not None:
+            os.environ["SEEDVR2_AWA_SPLIT"] = old
+    S = plan.info.sequence_tokens
+    vq, tq = qkv_blob(video, "a", 4), qkv_blob(text, "a", 4)
+    packed = mat3(HEAD_DIM, 3 * heads, S, 4)
+    cu = DeviceMat(dict(w=plan.info.window_count + 1, dims=1), plan.info.window_count + 1, 4)
+    roped = mat3(HEAD_DIM, 3 * heads, S, 4)
+    att = mat3(HEAD_DIM, heads, S, 4)
+    vo = video_out_blob(g.t, g.h, g.w, heads, HEAD_DIM, 4, False)
+    to = mat3(HEAD_DIM, heads, g.text_tokens, 4)
+    plan.pack(vq.blob, tq.blob, packed.blob, cu.blob)
+    plan.mmrope(packed.blob, roped.blob)
+    plan.window_attention(roped.blob, att.blob, A.COMPUTE_F32)
+    plan.unpack(att.blob, vo.blob, to.blob)
+    A.synchronize()
+    np.testing.assert_array_equal(read_video(vo, g.t, g.h, g.w, heads, HEAD_DIM), fv)
+    np.testing.assert_array_equal(read_mat3(to), ft)
