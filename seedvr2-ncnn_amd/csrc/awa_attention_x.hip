@@ -129,6 +129,20 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
     float* const rope_lds = reinterpret_cast<float*>(dyn_lds + kNormLdsBytes<NORM>);
     unsigned char* const row_dyn = dyn_lds + kNormLdsBytes<NORM> + rope_table_bytes(FUSED, p.rope_coords);
 
+    // RoPE table: its loads are issued first, before the work item is read
+    // (they do not depend on it), unconditionally (indices past the table
+    // are clamped to its last entry and their values dropped), and land in
+    // LDS after the Q and first-tile loads are in flight.
+    constexpr int kRopePerThread = (kMaxRopeCoords * kRopeRow + kThreads - 1) / kThreads;
+    float rope_reg[FUSED ? kRopePerThread : 1];
+    if constexpr (FUSED)
+    {
+        const int n = p.rope_coords * kRopeRow;
+#pragma unroll
+        for (int j = 0; j < kRopePerThread; j++)
+            rope_reg[j] = p.rope_cs[min(static_cast<int>(threadIdx.x) + j * kThreads, n - 1)];
+    }
+
     const WorkItem item = p.work[blockIdx.x];
     if (item.window < 0)
         return;
@@ -169,19 +183,6 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
         else
             return packed_base + (win.seq_start + i) * packed_row + qkv * packed_qkv + head_off;
     };
-
-    constexpr int kRopePerThread = (kMaxRopeCoords * kRopeRow + kThreads - 1) / kThreads;
-    float rope_reg[FUSED ? kRopePerThread : 1];
-    if constexpr (FUSED)
-    {
-        const int n = p.rope_coords * kRopeRow;
-#pragma unroll
-        for (int j = 0; j < kRopePerThread; j++)
-        {
-            const int e = tid + j * kThreads;
-            rope_reg[j] = e < n ? p.rope_cs[e] : 0.f;
-        }
-    }
 
     const int wave_row0 = item.row0 + wave * 32;
     const bool wave_active = wave * 32 < item.rows && wave_row0 < L;
