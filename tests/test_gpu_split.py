@@ -192,3 +192,38 @@ def test_single_window_text_written_directly(gpu, compute, elem, split_on):
     A.synchronize()
     np.testing.assert_array_equal(read_video(vo, g.t, g.h, g.w, heads, HEAD_DIM), fv)
     np.testing.assert_array_equal(read_mat3(to), ft)
+
+
+@pytest.mark.parametrize("compute,elem,split_on", [(A.COMPUTE_BF16, 2, True), (A.COMPUTE_F32, 4, False),
+                                                   (A.COMPUTE_F32, 4, True)])
+def test_single_window_padded_text_output(gpu, compute, elem, split_on):
+    """A text output with padded rows (cstep past H * d) cannot take the
+    direct write of a one-window layer's text rows: the text-mean (or, split,
+    the merge) kernel writes them instead, and the bits equal those of the
+    dense output (the mean of one row is that row)."""
+    g = geometry(CONFIGS["production_256"], False)
+    heads = 4
+    print(f"case single window padded text output compute={compute} elem={elem} split={split_on}", flush=True)
+    video, text = qkv_inputs(g, heads, HEAD_DIM, 20260905)
+    if compute == A.COMPUTE_BF16:
+        video, text = bf16_round(video), bf16_round(text)
+    dv, dt, split = run_fused(g, video, text, compute, elem, split_on=split_on)
+    assert (split > 1) == (split_on and compute == A.COMPUTE_F32)
+    old = os.environ.pop("SEEDVR2_AWA_SPLIT", None)
+    if not split_on:
+        os.environ["SEEDVR2_AWA_SPLIT"] = "0"
+    try:
+        plan = A.Plan(A.LayerParams(*g.args, g.text_tokens, g.shifted), heads=heads)
+        plan.upload()
+    finally:
+        os.environ.pop("SEEDVR2_AWA_SPLIT", None)
+        if old is not None:
+            os.environ["SEEDVR2_AWA_SPLIT"] = old
+    vq, tq = qkv_blob(video, "a", elem), qkv_blob(text, "a", elem)
+    vo = video_out_blob(g.t, g.h, g.w, heads, HEAD_DIM, elem, False)
+    cstep = heads * HEAD_DIM + 16 // elem
+    to = DeviceMat(dict(w=HEAD_DIM, h=heads, c=g.text_tokens, dims=3, cstep=cstep), g.text_tokens * cstep, elem)
+    plan.forward(vq.blob, tq.blob, vo.blob, to.blob, compute)
+    A.synchronize()
+    np.testing.assert_array_equal(read_video(vo, g.t, g.h, g.w, heads, HEAD_DIM), dv)
+    np.testing.assert_array_equal(read_mat3(to), dt)
