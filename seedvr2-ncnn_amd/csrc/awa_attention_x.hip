@@ -13,9 +13,9 @@
 //   the slice products d_s(q) d_t(k) with s + t = w over the 128 features.
 //   v_mfma_i32_32x32x32_i8 accumulates them in int32 exactly (each C_w stays
 //   below 2^23, so its conversion to fp32 is exact too), the dropped classes
-//   w > 5 weigh below 2^-30, and the classes are combined in fp32 from the
-//   smallest up, so a score carries one fp32 rounding, like a correctly
-//   rounded dot product.
+//   w > 5 weigh below 2^-30, and the classes are combined from the smallest
+//   up (C4 2^8 + C5 exactly in int32, then C3 and C2 in fp32), so a score
+//   carries one fp32 rounding, like a correctly rounded dot product.
 // - P V runs on bf16 MFMA with P = p1 + p2 + p3 and V = v1 + v2 + v3, three
 //   bf16 pieces each (all 24 bits of the fp32 value), products p1 (v1 + v2 +
 //   v3) + p2 (v1 + v2) + p3 v1 (the dropped ones weigh below 2^-24), fp32
@@ -468,9 +468,13 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
                 c4 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k[0], qs[2][c], c4, 0, 0, 0);
                 c5 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k[0], qs[3][c], c5, 0, 0, 0);
             }
+            // C4 2^8 + C5 is exact in int32 (|C4| <= 2^22, |C5| < 2^23), so
+            // its conversion is the one rounding of C4 + C5 / 2^8 (scaled by
+            // 2^8, which the next step folds into its factor).
 #pragma unroll
             for (int i = 0; i < 16; i++)
-                f[i] = fmaf(static_cast<float>(c5[i]), 1.f / 256.f, static_cast<float>(c4[i]));
+                f[i] = static_cast<float>(
+                    static_cast<int>((static_cast<uint32_t>(c4[i]) << 8) + static_cast<uint32_t>(c5[i])));
         }
     };
     auto scores_lo = [&](int buf, f32x16& f, f32x16& c2f) {
@@ -489,7 +493,7 @@ __global__ __launch_bounds__(WIDE ? 512 : 256, WIDE ? 1 : 2) void window_attenti
 #pragma unroll
             for (int i = 0; i < 16; i++)
             {
-                f[i] = fmaf(f[i], 1.f / 256.f, static_cast<float>(c3[i]));
+                f[i] = fmaf(f[i], 1.f / 65536.f, static_cast<float>(c3[i]));
                 c2f[i] = static_cast<float>(c2[i]);
             }
         }

@@ -92,3 +92,23 @@ def test_score_classes_fit_exact_int32_and_fp32():
     bound = {2: 64 * 64, 3: 2 * 64 * 128, 4: 2 * 64 * 128 + 128 * 128, 5: 2 * 64 * 128 + 2 * 128 * 128}
     for w, per_feature in bound.items():
         assert per_feature * 128 < 2**23, w
+
+
+def test_class_four_and_five_merge_exactly_in_int32():
+    """The exact-score kernel forms C4 * 2^8 + C5 in int32 and converts it
+    once: the sum stays below 2^31 at the class bounds, and its rounded
+    conversion divided by 2^8 equals the correctly rounded C4 + C5 / 2^8 (the
+    single fused multiply-add it replaces) for extreme and random classes."""
+    c4_max = 2 * 64 * 128 * 128 + 128 * 128 * 128
+    c5_max = (2 * 64 * 128 + 2 * 128 * 128) * 128
+    assert c4_max * 256 + c5_max < 2**31
+    rng = np.random.default_rng(5)
+    c4 = np.concatenate([rng.integers(-c4_max, c4_max + 1, 200000), [c4_max, -c4_max, 0, 1, -1]])
+    c5 = np.concatenate([rng.integers(-c5_max, c5_max + 1, 200000), [c5_max, -c5_max, 255, -255, 127]])
+    merged = (c4 * 256 + c5).astype(np.int64)
+    assert np.all(np.abs(merged) < 2**31)
+    got = merged.astype(np.float32) / np.float32(256)
+    # C4 + C5 / 2^8 is exact in float64 (at most 31 significant bits); its
+    # float32 rounding is the fused multiply-add's result.
+    want = (c4.astype(np.float64) + c5.astype(np.float64) / 256.0).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
