@@ -547,9 +547,12 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
     const int krow = col; // K rows are stored key-permuted
 
     // S^T = K Q^T of one tile: one 32x32 block per 32 keys; chains interleaved.
-    auto scores = [&](f32x16 (&s)[kBlocks], int buf) {
+    // nb: 32-key blocks of the tile that hold keys of the window (1 on a
+    // last tile of at most 32 keys, whose second block would be all masked).
+    auto scores = [&](f32x16 (&s)[kBlocks], int buf, auto nb) {
+        constexpr int NB = decltype(nb)::value;
 #pragma unroll
-        for (int b = 0; b < kBlocks; b++)
+        for (int b = 0; b < NB; b++)
 #pragma unroll
             for (int i = 0; i < 16; i++)
                 s[b][i] = 0.f;
@@ -576,18 +579,18 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
 #pragma unroll
             for (int c = 0; c < kAhead; c++)
 #pragma unroll
-                for (int b = 0; b < kBlocks; b++)
+                for (int b = 0; b < NB; b++)
                     ka[b][c] = *reinterpret_cast<const bf16x8*>(ks + b * 32 * kKPitch + 16 * c);
 #pragma unroll
             for (int c = 0; c < 8; c++)
             {
                 if (c + kAhead < 8)
 #pragma unroll
-                    for (int b = 0; b < kBlocks; b++)
+                    for (int b = 0; b < NB; b++)
                         ka[b][c + kAhead] = *reinterpret_cast<const bf16x8*>(ks + b * 32 * kKPitch + 16 * (c + kAhead));
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int b = 0; b < kBlocks; b++)
+                for (int b = 0; b < NB; b++)
                     s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[b][c], qb[c], c == 0 ? c0 : s[b], 0, 0, 0);
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -622,12 +625,13 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
     // wave-uniform branch); otherwise every tile rescales, without a branch,
     // so that the code can be interleaved with independent MFMA work.
     // may_mask: the tile can be the ragged last one.
-    auto softmax = [&](f32x16 (&s)[kBlocks], int tile, auto lazy, auto may_mask) {
+    auto softmax = [&](f32x16 (&s)[kBlocks], int tile, auto lazy, auto may_mask, auto nb) {
+        constexpr int NB = decltype(nb)::value;
         if (decltype(may_mask)::value && tile == tiles - 1 && (L % KT))
         {
             const int key0 = tile * KT + 8 * half;
 #pragma unroll
-            for (int b = 0; b < kBlocks; b++)
+            for (int b = 0; b < NB; b++)
 #pragma unroll
                 for (int i = 0; i < 16; i++)
                     if (key0 + 32 * b + 16 * (i >> 3) + (i & 7) >= L)
@@ -635,7 +639,7 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
         }
         float tile_max = s[0][0];
 #pragma unroll
-        for (int b = 0; b < kBlocks; b++)
+        for (int b = 0; b < NB; b++)
 #pragma unroll
             for (int i = 0; i < 16; i++)
                 tile_max = fmaxf(tile_max, s[b][i]);
@@ -658,7 +662,7 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
                 }
                 row_max += delta;
 #pragma unroll
-                for (int b = 0; b < kBlocks; b++)
+                for (int b = 0; b < NB; b++)
 #pragma unroll
                     for (int i = 0; i < 16; i++)
                         s[b][i] -= delta;
@@ -668,7 +672,7 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
             }
             // The row sum is taken in pv(), over the bf16 probabilities.
 #pragma unroll
-            for (int b = 0; b < kBlocks; b++)
+            for (int b = 0; b < NB; b++)
 #pragma unroll
                 for (int i = 0; i < 16; i++)
                     s[b][i] = __builtin_amdgcn_exp2f(s[b][i]);
@@ -688,7 +692,7 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
         }
         float psum = 0.f;
 #pragma unroll
-        for (int b = 0; b < kBlocks; b++)
+        for (int b = 0; b < NB; b++)
 #pragma unroll
             for (int i = 0; i < 16; i++)
             {
@@ -699,12 +703,13 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
     };
 
     // O^T += V^T P^T of one tile.
-    auto pv = [&](const f32x16 (&s)[kBlocks], int buf) {
+    auto pv = [&](const f32x16 (&s)[kBlocks], int buf, auto nb) {
+        constexpr int NB = decltype(nb)::value;
         if constexpr (BF16)
         {
             bf16x8 pb[2 * kBlocks];
 #pragma unroll
-            for (int b = 0; b < kBlocks; b++)
+            for (int b = 0; b < NB; b++)
 #pragma unroll
                 for (int e = 0; e < 8; e++)
                 {
@@ -718,7 +723,7 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
                 // denominator share the rounding.
                 const bf16x2 ones = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
 #pragma unroll
-                for (int j = 0; j < 2 * kBlocks; j++)
+                for (int j = 0; j < 2 * NB; j++)
 #pragma unroll
                     for (int q = 0; q < 4; q++)
                     {
@@ -736,7 +741,7 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
             const uint16_t* vt = reinterpret_cast<const uint16_t*>(v_lds + buf * kVBytes) +
                                  (8 * half + ((lane & 15) >> 2)) * kVPitch + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 #pragma unroll
-            for (int j = 0; j < 2 * kBlocks; j++)
+            for (int j = 0; j < 2 * NB; j++)
             {
                 bf16x8 va[4];
 #pragma unroll
@@ -787,6 +792,8 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
 
     using Yes = std::integral_constant<bool, true>;
     using No = std::integral_constant<bool, false>;
+    using AllBlocks = std::integral_constant<int, kBlocks>;
+    using OneBlock = std::integral_constant<int, 1>;
     if constexpr (PIPE)
     {
         // Software pipeline, one barrier per tile, K and V double-buffered
@@ -808,7 +815,7 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
         __syncthreads();
         f32x16 s[kBlocks];
         if (wave_active)
-            scores(s, 0);
+            scores(s, 0, AllBlocks());
         __syncthreads(); // K buffer 0 is rewritten in step 0
         for (int tile = 0; tile < last; tile++)
         {
@@ -816,11 +823,11 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
             if (wave_active)
             {
                 f32x16 sn[kBlocks];
-                scores(sn, buf ^ 1);
-                softmax(s, tile, std::integral_constant<bool, BF16>(), No());
+                scores(sn, buf ^ 1, AllBlocks());
+                softmax(s, tile, std::integral_constant<bool, BF16>(), No(), AllBlocks());
                 store_v(buf ^ 1);
                 load_v(min(tile + 2, last));
-                pv(s, buf);
+                pv(s, buf, AllBlocks());
                 store_k(min(tile + 2, last), buf);
                 load_k(min(tile + 3, last));
 #pragma unroll
@@ -838,16 +845,20 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
         }
         if (wave_active)
         {
-            softmax(s, last, std::integral_constant<bool, BF16>(), Yes());
-            pv(s, last & 1);
+            softmax(s, last, std::integral_constant<bool, BF16>(), Yes(), AllBlocks());
+            pv(s, last & 1, AllBlocks());
         }
     }
     else
     {
         // Step t: stage tile t into LDS, refill the registers with tile t+1's
-        // loads, then scores, softmax and PV of tile t.
-        for (int tile = t_begin; tile < t_end; tile++)
-        {
+        // loads, then scores, softmax and PV of tile t. A last tile of at
+        // most 32 keys runs its first score block only (the second would be
+        // masked whole: probabilities 0, the same bits); it is peeled off the
+        // loop so that the loop body keeps one form. (Kernels on fp32 inputs,
+        // whose register stages leave no room for the second form, keep the
+        // loop whole.)
+        auto step = [&](int tile, auto nb) {
             store_tile(tile, 0);
             __syncthreads();
             if (tile + 1 < t_end)
@@ -855,12 +866,19 @@ __global__ __launch_bounds__(VARIANT != kVariantNarrow ? 512 : 256,
             if (wave_active)
             {
                 f32x16 s[kBlocks];
-                scores(s, 0);
-                softmax(s, tile, Yes(), Yes());
-                pv(s, 0);
+                scores(s, 0, nb);
+                softmax(s, tile, Yes(), Yes(), nb);
+                pv(s, 0, nb);
             }
             __syncthreads();
-        }
+        };
+        const bool short_last = kBlocks > 1 && sizeof(TIn) == 2 && L - (t_end - 1) * KT <= 32;
+        const int full_end = short_last ? t_end - 1 : t_end;
+        for (int tile = t_begin; tile < full_end; tile++)
+            step(tile, AllBlocks());
+        if constexpr (kBlocks > 1 && sizeof(TIn) == 2)
+            if (short_last)
+                step(t_end - 1, OneBlock());
     }
 
     if (p.split > 1)
