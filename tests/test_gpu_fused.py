@@ -242,3 +242,22 @@ def test_text_mean_repeated_launches(gpu):
                     first[key] = (got_v, got_t)
                 np.testing.assert_array_equal(got_v, first[key][0])
                 np.testing.assert_array_equal(got_t, first[key][1])
+
+
+# Layers whose windows end in a last key tile of at most 32 keys (shifted: the
+# 33-frame layer's windows of 80, 96 and 160 rows, the 5-frame clip's of 96, a
+# ragged grid's of 140 and 406). On bf16
+# inputs the bf16 kernel runs such a tile's first score block only; on fp32
+# inputs it runs the whole tile with the second block masked. Fed the same
+# bf16-representable values, the two must agree bit for bit.
+@pytest.mark.parametrize("params", [CONFIGS["clip_9x16x16"], CONFIGS["clip_2x16x16"], RAGGED[1]])
+def test_short_last_tile_same_bits(gpu, params):
+    g = geometry(params, True)
+    print(f"case short last tile {params} shifted", flush=True)
+    video, text = qkv_inputs(g, 4, HEAD_DIM, 20260901)
+    video, text = bf16_round(video), bf16_round(text)
+    v2, t2 = run_fused(g, video, text, A.COMPUTE_BF16, in_elem=2, out_elem=2)
+    v4, t4 = run_fused(g, video, text, A.COMPUTE_BF16, in_elem=4, out_elem=2)
+    assert np.array_equal(v2, v4) and np.array_equal(t2, t4)
+    ref_v, ref_t = O.awa_layer(g, video, text, 4, HEAD_DIM)
+    assert rel_err(v2, ref_v) <= BF16_RTOL and rel_err(t2, ref_t) <= BF16_RTOL
